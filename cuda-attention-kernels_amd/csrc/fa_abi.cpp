@@ -1,0 +1,169 @@
+// extern "C" entry points of libfused_attn_hip.so: argument validation, error
+// reporting, device checks.  Replaces the reference's pybind layer
+// (csrc/bindings.cpp:10-96): the checks mirror check_inputs
+// (csrc/bindings.cpp:35-50) and the mma preconditions (:66-74), but failures
+// are returned as fa_status codes with a thread-local message instead of
+// exceptions, and the caller owns every allocation.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/fused_attn_hip.h"
+#include "fa_internal.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+fa_status fail(fa_status code, const char* msg) {
+  g_last_error = msg;
+  return code;
+}
+
+bool aligned(const void* p, size_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+size_t dtype_bytes(int32_t dt) {
+  switch (dt) {
+    case FA_DTYPE_F16:
+    case FA_DTYPE_BF16:
+      return 2;
+    case FA_DTYPE_F32:
+      return 4;
+    case FA_DTYPE_FP8_E4M3:
+      return 1;
+    default:
+      return 0;
+  }
+}
+
+// Validation shared by every forward entry point.  `fp8_ok` allows FP8 K/V.
+fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok) {
+  if (p == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params is NULL");
+  if (p->batch < 0 || p->heads_q <= 0 || p->heads_kv <= 0 || p->seqlen_q < 0 || p->seqlen_k < 0 ||
+      p->head_dim <= 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "sizes must be non-negative (heads and head_dim positive)");
+  if (p->heads_q % p->heads_kv != 0) return fail(FA_ERR_INVALID_ARGUMENT, "H_q must be a multiple of H_kv");
+  if (dtype_bytes(p->dtype) == 0 || dtype_bytes(p->kv_dtype) == 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "unknown dtype code");
+  if (p->dtype != FA_DTYPE_F16 && p->dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_UNSUPPORTED, "q/o dtype must be float16 or bfloat16 for the MFMA kernels");
+  if (p->kv_dtype != p->dtype) {
+    if (!(fp8_ok && p->kv_dtype == FA_DTYPE_FP8_E4M3))
+      return fail(FA_ERR_INVALID_ARGUMENT, "k/v dtype must match q (or be float8_e4m3fn on the split-K path)");
+  }
+  if (p->head_dim != 64 && p->head_dim != 128)
+    return fail(FA_ERR_UNSUPPORTED, "head_dim must be 64 or 128 for the MFMA kernels");
+  if (p->kv_dtype == FA_DTYPE_FP8_E4M3 && (p->k_scale == nullptr || p->v_scale == nullptr))
+    return fail(FA_ERR_INVALID_ARGUMENT, "FP8 K/V needs k_scale and v_scale");
+  if (!(p->scale == p->scale)) return fail(FA_ERR_INVALID_ARGUMENT, "scale is NaN");
+
+  if (varlen) {
+    if (p->cu_seqlens_q == nullptr || p->cu_seqlens_k == nullptr)
+      return fail(FA_ERR_INVALID_ARGUMENT, "varlen needs cu_seqlens_q and cu_seqlens_k");
+    if (p->max_seqlen_q < 0 || p->max_seqlen_k < 0)
+      return fail(FA_ERR_INVALID_ARGUMENT, "max_seqlen must be non-negative");
+    if (p->lse != nullptr) return fail(FA_ERR_UNSUPPORTED, "LSE output is not available on the varlen path");
+  }
+  const bool empty = p->batch == 0 || (varlen ? p->max_seqlen_q == 0 : p->seqlen_q == 0);
+  if (empty) return FA_OK;
+
+  const bool no_keys = varlen ? p->max_seqlen_k == 0 : p->seqlen_k == 0;
+  if (p->q == nullptr || p->o == nullptr || (!no_keys && (p->k == nullptr || p->v == nullptr)))
+    return fail(FA_ERR_INVALID_ARGUMENT, "q, k, v and o must be non-NULL");
+  // 16-byte vector loads of Q rows and K/V rows; 8-byte stores of O.
+  const int64_t qvec = 8, kvvec = (int64_t)(16 / dtype_bytes(p->kv_dtype)), ovec = 4;
+  if (!aligned(p->q, 16) || !aligned(p->k, 16) || !aligned(p->v, 16) || !aligned(p->o, 8))
+    return fail(FA_ERR_INVALID_ARGUMENT, "q/k/v must be 16-byte aligned and o 8-byte aligned");
+  if ((!varlen && (p->q_stride_b % qvec)) || p->q_stride_h % qvec || p->q_stride_n % qvec)
+    return fail(FA_ERR_INVALID_ARGUMENT, "q strides must be multiples of 8 elements (16 bytes)");
+  if ((!varlen && (p->k_stride_b % kvvec || p->v_stride_b % kvvec)) || p->k_stride_h % kvvec ||
+      p->k_stride_n % kvvec || p->v_stride_h % kvvec || p->v_stride_n % kvvec)
+    return fail(FA_ERR_INVALID_ARGUMENT, "k/v strides must be multiples of 16 bytes");
+  if ((!varlen && (p->o_stride_b % ovec)) || p->o_stride_h % ovec || p->o_stride_n % ovec)
+    return fail(FA_ERR_INVALID_ARGUMENT, "o strides must be multiples of 4 elements (8 bytes)");
+  return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream) {
+  g_last_error.clear();
+  fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/false);
+  if (st != FA_OK) return st;
+  if (p->lse != nullptr && (p->lse_stride_b < 0 || p->lse_stride_h < 0))
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
+  const char* err = nullptr;
+  st = fa::run_fwd(*p, false, reinterpret_cast<hipStream_t>(stream), &err);
+  if (st != FA_OK) return fail(st, err ? err : "launch failed");
+  return FA_OK;
+}
+
+fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream) {
+  g_last_error.clear();
+  fa_status st = validate(p, /*varlen=*/true, /*fp8_ok=*/false);
+  if (st != FA_OK) return st;
+  const char* err = nullptr;
+  st = fa::run_fwd(*p, true, reinterpret_cast<hipStream_t>(stream), &err);
+  if (st != FA_OK) return fail(st, err ? err : "launch failed");
+  return FA_OK;
+}
+
+size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q, int32_t head_dim,
+                                 int32_t num_splits) {
+  if (batch <= 0 || heads_q <= 0 || seqlen_q <= 0 || head_dim <= 0 || num_splits <= 0) return 0;
+  const size_t rows = (size_t)batch * (size_t)heads_q * (size_t)seqlen_q * (size_t)num_splits;
+  return rows * ((size_t)head_dim + 2) * sizeof(float);
+}
+
+fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  g_last_error.clear();
+  fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/true);
+  if (st != FA_OK) return st;
+  if (p->lse != nullptr) return fail(FA_ERR_UNSUPPORTED, "LSE output is not available on the split-K path");
+  if (split_len <= 0 || split_len % 64 != 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "split_len must be a positive multiple of 64");
+  if (p->batch == 0 || p->seqlen_q == 0) return FA_OK;
+  const int32_t splits = p->seqlen_k > 0 ? (p->seqlen_k + split_len - 1) / split_len : 1;
+  const size_t need = fa_splitk_workspace_bytes(p->batch, p->heads_q, p->seqlen_q, p->head_dim, splits);
+  if (workspace == nullptr || workspace_bytes < need) {
+    char buf[160];
+    snprintf(buf, sizeof(buf), "split-K workspace too small: need %zu bytes, got %zu", need,
+             workspace == nullptr ? (size_t)0 : workspace_bytes);
+    return fail(FA_ERR_WORKSPACE, buf);
+  }
+  if (!aligned(workspace, 16)) return fail(FA_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+  if (p->kv_dtype == FA_DTYPE_FP8_E4M3 && (p->scale_stride_b < 0 || p->scale_stride_h < 0))
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative FP8 scale stride");
+  const char* err = nullptr;
+  st = fa::run_splitk(*p, split_len, workspace, reinterpret_cast<hipStream_t>(stream), &err);
+  if (st != FA_OK) return fail(st, err ? err : "launch failed");
+  return FA_OK;
+}
+
+int32_t fa_choose_num_splits(int32_t batch, int32_t heads, int32_t seqlen_k, int32_t seqlen_q, int32_t num_cus) {
+  if (seqlen_q > 64) return 1;  // prefill-sized queries already fill the GPU
+  const int64_t programs = (int64_t)batch * heads;
+  int64_t want = (2 * (int64_t)num_cus) / (programs > 1 ? programs : 1);
+  if (want < 1) want = 1;
+  int64_t cap = seqlen_k / 256;
+  if (cap < 1) cap = 1;
+  int64_t n = want < cap ? want : cap;
+  return (int32_t)(n < 64 ? n : 64);
+}
+
+int32_t fa_device_supported(int32_t device) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+const char* fa_last_error(void) { return g_last_error.c_str(); }
+
+int32_t fa_abi_version(void) { return FA_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,147 @@
+// Device helpers for the gfx950 (CDNA4) attention kernels: vector types, MFMA
+// wrappers, fp8 decode, LDS transpose reads and cross-lane reductions.
+//
+// Lane layouts (wave64) used throughout, verified on MI355X:
+//   v_mfma_f32_32x32x16_{bf16,f16}:  A[i][k]: lane l holds i = l%32, k = 8*(l/32) + 0..7
+//                                    B[k][j]: lane l holds j = l%32, k = 8*(l/32) + 0..7
+//                                    C[i][j]: lane l, acc r holds i = 8*(r/4) + 4*(l/32) + r%4, j = l%32
+//   ds_read_b64_tr_b16: in each 16-lane group, lane i receives element (i%4) of the
+//                       8-byte rows addressed by lanes (i/4) + 4e, e = 0..3.
+//   v_permlane32_swap(x, x): {r0, r1} with max(r0, r1) = max(x[l], x[l^32]).
+//   v_cvt_pk_f32_fp8: OCP float8_e4m3fn -> fp32, exact for all 256 codes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
+typedef _Float16 f16x8 __attribute__((__vector_size__(16)));
+typedef __bf16 bf16x2 __attribute__((__vector_size__(4)));
+typedef _Float16 f16x2 __attribute__((__vector_size__(4)));
+typedef float f32x16 __attribute__((__vector_size__(64)));
+typedef float f32x4 __attribute__((__vector_size__(16)));
+typedef float f32x2 __attribute__((__vector_size__(8)));
+typedef short i16x4 __attribute__((__vector_size__(8)));
+typedef uint32_t u32x4 __attribute__((__vector_size__(16)));
+typedef uint32_t u32x2 __attribute__((__vector_size__(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element tags.  Storage is always 16-bit (or 8-bit for fp8) in memory.
+struct BF16 {
+  static constexpr int bytes = 2;
+};
+struct F16 {
+  static constexpr int bytes = 2;
+};
+struct FP8 {  // OCP float8_e4m3fn K/V cache
+  static constexpr int bytes = 1;
+};
+
+template <class E>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c);
+
+template <>
+__device__ __forceinline__ f32x16 mfma32<BF16>(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<F16>(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
+// Round-to-nearest-even pack of two fp32 into one dword of 16-bit values (lo first).
+template <class E>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
+  f16x2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// 16-bit -> fp32 (exact).
+template <class E>
+__device__ __forceinline__ float lo_f32(uint32_t w);
+template <class E>
+__device__ __forceinline__ float hi_f32(uint32_t w);
+template <>
+__device__ __forceinline__ float lo_f32<BF16>(uint32_t w) {
+  return __builtin_bit_cast(float, w << 16);
+}
+template <>
+__device__ __forceinline__ float hi_f32<BF16>(uint32_t w) {
+  return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ float lo_f32<F16>(uint32_t w) {
+  return (float)__builtin_bit_cast(f16x2, w)[0];
+}
+template <>
+__device__ __forceinline__ float hi_f32<F16>(uint32_t w) {
+  return (float)__builtin_bit_cast(f16x2, w)[1];
+}
+
+// Four e4m3fn bytes (one dword) -> two dwords of packed 16-bit E values.  Exact:
+// every e4m3fn value is representable in bf16 and in fp16.
+template <class E>
+__device__ __forceinline__ u32x2 fp8x4_to_e(uint32_t w) {
+  const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  u32x2 r;
+  r[0] = pack2<E>(a[0], a[1]);
+  r[1] = pack2<E>(b[0], b[1]);
+  return r;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
+// 8-byte transposed LDS read (ds_read_b64_tr_b16).  `p` points into __shared__ memory.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef i16x4 __attribute__((address_space(3))) * lds_v4_ptr;
+  typedef uint16_t __attribute__((address_space(3))) * lds_u16_ptr;
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4_ptr)((lds_u16_ptr)p));
+  return __builtin_bit_cast(u32x2, r);
+#else
+  (void)p;
+  return u32x2{0, 0};
+#endif
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ void st8(void* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// Physical workgroup id -> logical id such that each XCD (8 per MI355X, each
+// with its own L2) receives a contiguous range of logical ids.  Workgroups are
+// dispatched round-robin over XCDs, so id p runs on XCD p % 8.
+__device__ __forceinline__ int xcd_remap(int pid, int total) {
+  constexpr int kXcds = 8;
+  const int q = total / kXcds, r = total % kXcds;
+  const int xcd = pid % kXcds, slot = pid / kXcds;
+  return xcd * q + (xcd < r ? xcd : r) + slot;
+}
+
+}  // namespace fa

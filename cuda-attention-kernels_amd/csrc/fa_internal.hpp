@@ -1,0 +1,56 @@
+// Internal interface between the C ABI (fa_abi.cpp) and the kernel launchers
+// (fa_kernels.hip).  Not part of the public header.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/fused_attn_hip.h"
+
+namespace fa {
+
+// Kernel arguments of the FA2 tile kernel, passed by value.  Pointers are raw
+// device pointers; strides are in elements of the pointed-to type.
+struct TileArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;     // prefill: output in the q dtype; split-K: fp32 partials [rows, S, D]
+  float* ml;   // split-K: (max, sum) pairs [rows, S, 2]
+  float* lse;  // prefill: optional natural-log LSE
+  const float* k_scale;
+  const float* v_scale;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int64_t sqb, sqh, sqn, skb, skh, skn, svb, svh, svn, sob, soh, son;
+  int64_t slb, slh;
+  int64_t ssb, ssh;
+  int32_t hq, hkv, group;
+  int32_t nq, nk;  // dense lengths; varlen: maxima
+  int32_t n_rowblk;
+  int32_t n_split, split_len;
+  int32_t total;  // workgroups in the grid
+  float qk_scale; // softmax scale * log2(e)
+  int32_t causal;
+  int32_t varlen;
+};
+
+struct CombineArgs {
+  const float* opart;
+  const float* ml;
+  void* o;
+  int64_t sob, soh, son;
+  int32_t hq, nq, n_split;
+};
+
+// Number of rows (q-heads x queries) one split-K workgroup covers, and the
+// workgroup shape chosen for a given row count G*Nq.
+int splitk_waves_for_rows(int rows);
+
+// Launchers.  They assume fa_abi.cpp has validated `p`.
+fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
+fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,
+                     const char** err);
+
+}  // namespace fa

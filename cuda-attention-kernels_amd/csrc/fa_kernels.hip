@@ -1,0 +1,593 @@
+// FlashAttention-2 forward kernels for MI355X (gfx950).
+//
+// One tile kernel serves two call shapes of the reference:
+//   * prefill (dense and varlen): the reference's attn_fwd_mma_kernel
+//     (csrc/flash_attn_mma.cu:63-242) and _attn_fwd_kernel
+//     (fused_attn/triton_fwd.py:85-172);
+//   * split-K flash-decoding: _attn_splitk_kernel
+//     (fused_attn/triton_splitk.py:29-96), including the FP8 K/V variant of
+//     _attn_fp8_kernel (fused_attn/fp8.py:59-122).
+// plus the log-sum-exp combine kernel (_splitk_combine_kernel,
+// fused_attn/triton_splitk.py:99-127).
+//
+// Work decomposition.  A workgroup has NW waves; wave w owns 32 "rows" of a
+// row space.  In prefill a row is a query of one q-head; in split-K a row is a
+// (q-head of the kv group, query) pair, so the G = Hq/Hkv heads that share a
+// kv-head read each K/V tile once.  K/V stream through LDS in BN-key tiles,
+// double-buffered through registers: the global loads of tile t+1 are issued
+// before tile t is multiplied and land in the other LDS stage afterwards.
+//
+// Per tile, per wave (S^T orientation, so the softmax is lane-local):
+//   S^T = K Q^T   v_mfma_f32_32x32x16: A = K rows from LDS, B = Q from VGPRs.
+//                 The C fragment gives each lane one row (query) and 16 keys.
+//                 The A-row -> key map swaps the middle quads of every 16 keys,
+//                 so a lane's keys come out as 8 contiguous keys per 16-key step.
+//   softmax       online, base 2, scale*log2(e) folded in; max/sum need only the
+//                 partner lane l^32 (v_permlane32_swap).
+//   P^T           the fp32 C fragment is rounded to 16 bits in place and is the
+//                 B operand of the next MFMA: P never leaves VGPRs.
+//   O^T += V^T P^T  A = V^T read from row-major LDS with ds_read_b64_tr_b16.
+// Causal masking is bottom-right aligned (reference.py:24-33); only tiles that
+// cross a row's diagonal or the key end are masked element-wise, and a wave
+// stops issuing MFMAs past its own last visible key.
+#include <float.h>
+
+#include <mutex>
+
+#include "fa_device.hpp"
+#include "fa_internal.hpp"
+
+namespace fa {
+
+template <int D, int BN, int KVB>
+struct TileShape {
+  static constexpr int KLD = D + 8;   // K row stride in LDS (elements): 16 B pad, conflict-free b128 row reads
+  static constexpr int VLD = D + 16;  // V row stride: 32 B pad, conflict-free transposed reads
+  static constexpr int KTILE = BN * KLD;
+  static constexpr int VTILE = BN * VLD;
+  static constexpr int STAGE = KTILE + VTILE;
+  static constexpr size_t LDS_BYTES = 2 * STAGE * 2;
+};
+
+template <int D, class E, class KV, int NW, int BN, bool SPLIT>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) attn_tile_kernel(const TileArgs a) {
+  constexpr int NT = NW * 64;
+  using Shape = TileShape<D, BN, KV::bytes>;
+  constexpr int KLD = Shape::KLD, VLD = Shape::VLD, KTILE = Shape::KTILE, STAGE = Shape::STAGE;
+  constexpr int KB = BN / 32;   // 32-key MFMA blocks per tile
+  constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
+  constexpr int DB = D / 32;    // 32-wide d blocks of O^T
+  constexpr int EPC = 16 / KV::bytes;  // K/V elements per 16-byte global chunk
+  constexpr int CPR = D / EPC;         // chunks per key row
+  constexpr int CPT = BN * CPR / NT;   // chunks per thread per tile
+  static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
+  static_assert((BN * CPR) % NT == 0, "tile must split evenly over the workgroup");
+  constexpr float NEG_INF = -__builtin_inff();
+
+  extern __shared__ __align__(16) uint16_t smem[];
+
+  // ---- work item -------------------------------------------------------------------
+  const int logical = xcd_remap((int)blockIdx.x, a.total);
+  int b, kvh, rb, split = 0, hq_fixed = 0;
+  if (SPLIT) {
+    rb = logical % a.n_rowblk;
+    int t = logical / a.n_rowblk;
+    split = t % a.n_split;
+    t /= a.n_split;
+    kvh = t % a.hkv;
+    b = t / a.hkv;
+  } else {
+    const int mrev = logical % a.n_rowblk;
+    int t = logical / a.n_rowblk;
+    const int gi = t % a.group;
+    t /= a.group;
+    kvh = t % a.hkv;
+    b = t / a.hkv;
+    hq_fixed = kvh * a.group + gi;
+    rb = a.causal ? (a.n_rowblk - 1 - mrev) : mrev;  // heaviest causal blocks first
+  }
+
+  int seq_q = a.nq, seq_k = a.nk;
+  int64_t qtok0 = 0, ktok0 = 0;
+  if (!SPLIT && a.varlen) {
+    const int qs = a.cu_q[b], ks = a.cu_k[b];
+    seq_q = a.cu_q[b + 1] - qs;
+    seq_k = a.cu_k[b + 1] - ks;
+    qtok0 = qs;
+    ktok0 = ks;
+  }
+  const int R = SPLIT ? a.group * seq_q : seq_q;  // rows in this item's row space
+  const int r0 = rb * NW * 32;
+  if (r0 >= R) return;  // uniform over the workgroup (zero-length sequences exit here)
+  const int offset = seq_k - seq_q;
+
+  int klo = 0, khi = seq_k;
+  if (SPLIT) {
+    klo = split * a.split_len;
+    khi = min(seq_k, klo + a.split_len);
+  }
+  if (a.causal) {
+    const int re = min(r0 + NW * 32, R);
+    int qmax;
+    if (SPLIT) {
+      qmax = (re - r0 >= seq_q || (r0 % seq_q) > ((re - 1) % seq_q)) ? seq_q - 1 : (re - 1) % seq_q;
+    } else {
+      qmax = re - 1;
+    }
+    khi = min(khi, qmax + offset + 1);
+  }
+  const int n_tiles = khi > klo ? (khi - klo + BN - 1) / BN : 0;
+
+  // ---- lane roles ------------------------------------------------------------------
+  const int tid = (int)threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 5, j = lane & 31;
+  const int wr0 = r0 + wave * 32;
+  const int row = wr0 + j;
+  const bool row_ok = row < R;
+  const bool wave_active = wr0 < R;
+  int hq = hq_fixed, qi = row;
+  if (SPLIT) {
+    hq = kvh * a.group + (row_ok ? row / seq_q : 0);
+    qi = row_ok ? row % seq_q : 0;
+  }
+  // Keys visible to every row of the wave need no element-wise mask; keys at or
+  // beyond wave_khi are visible to no row of the wave.
+  int wave_khi = khi, mask_from = khi;
+  if (a.causal && wave_active) {
+    const int we = min(wr0 + 32, R);
+    int qlo, qhi;
+    if (SPLIT) {
+      if (we - wr0 >= seq_q || (wr0 % seq_q) > ((we - 1) % seq_q)) {
+        qlo = 0;
+        qhi = seq_q - 1;
+      } else {
+        qlo = wr0 % seq_q;
+        qhi = (we - 1) % seq_q;
+      }
+    } else {
+      qlo = wr0;
+      qhi = we - 1;
+    }
+    wave_khi = min(khi, qhi + offset + 1);
+    mask_from = min(khi, qlo + offset + 1);
+  }
+
+  const uint8_t* kbase =
+      (const uint8_t*)a.k + ((int64_t)b * a.skb + (int64_t)kvh * a.skh + ktok0 * a.skn) * KV::bytes;
+  const uint8_t* vbase =
+      (const uint8_t*)a.v + ((int64_t)b * a.svb + (int64_t)kvh * a.svh + ktok0 * a.svn) * KV::bytes;
+  const float* ksc = nullptr;
+  const float* vsc = nullptr;
+  if (KV::bytes == 1) {
+    ksc = a.k_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
+    vsc = a.v_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
+  }
+
+  // ---- Q fragments (B operand of S^T), resident for the whole kernel -------------
+  u32x4 qf[KS];
+  {
+    const uint16_t* qp =
+        (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + (qtok0 + qi) * a.sqn + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = row_ok ? ld16(qp + 16 * s) : u32x4{0, 0, 0, 0};
+  }
+
+  // ---- K/V staging: global -> VGPR -> LDS ----------------------------------------
+  u32x4 kr[CPT], vr[CPT];
+  auto gload = [&](int n0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * NT;
+      const int key = c / CPR, dc = c % CPR;
+      const int n = n0 + key;
+      if (n < khi) {
+        kr[i] = ld16(kbase + ((int64_t)n * a.skn + dc * EPC) * KV::bytes);
+        vr[i] = ld16(vbase + ((int64_t)n * a.svn + dc * EPC) * KV::bytes);
+      } else {  // zero-fill: masked keys must not carry NaN/Inf into P*V
+        kr[i] = u32x4{0, 0, 0, 0};
+        vr[i] = u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto lstore = [&](int stage) {
+    uint16_t* Ks = smem + stage * STAGE;
+    uint16_t* Vs = Ks + KTILE;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * NT;
+      const int key = c / CPR, dc = c % CPR;
+      if constexpr (KV::bytes == 2) {
+        st16(Ks + key * KLD + dc * 8, kr[i]);
+        st16(Vs + key * VLD + dc * 8, vr[i]);
+      } else {
+        const u32x2 k0 = fp8x4_to_e<E>(kr[i][0]), k1 = fp8x4_to_e<E>(kr[i][1]);
+        const u32x2 k2 = fp8x4_to_e<E>(kr[i][2]), k3 = fp8x4_to_e<E>(kr[i][3]);
+        st16(Ks + key * KLD + dc * 16, u32x4{k0[0], k0[1], k1[0], k1[1]});
+        st16(Ks + key * KLD + dc * 16 + 8, u32x4{k2[0], k2[1], k3[0], k3[1]});
+        const u32x2 v0 = fp8x4_to_e<E>(vr[i][0]), v1 = fp8x4_to_e<E>(vr[i][1]);
+        const u32x2 v2 = fp8x4_to_e<E>(vr[i][2]), v3 = fp8x4_to_e<E>(vr[i][3]);
+        st16(Vs + key * VLD + dc * 16, u32x4{v0[0], v0[1], v1[0], v1[1]});
+        st16(Vs + key * VLD + dc * 16 + 8, u32x4{v2[0], v2[1], v3[0], v3[1]});
+      }
+    }
+  };
+
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+  float m_run = NEG_INF, l_run = 0.f;
+
+  // A-operand row j of S^T reads key krow(j): swap the middle two quads of each 16.
+  const int krow = (j & 0x13) | ((j & 4) << 1) | ((j & 8) >> 1);
+  // ds_read_b64_tr_b16 addressing for the V^T operand
+  const int tr_i = lane & 15, tr_dh = (lane >> 4) & 1;
+  const int tr_off = (8 * g + (tr_i >> 2)) * VLD + 16 * tr_dh + 4 * (tr_i & 3);
+
+  if (n_tiles > 0) {
+    gload(klo);
+    lstore(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < n_tiles; ++t) {
+    const int n0 = klo + t * BN;
+    if (t + 1 < n_tiles) gload(n0 + BN);
+
+    if (wave_active && n0 < wave_khi) {
+      const uint16_t* Ks = smem + (t & 1) * STAGE;
+      const uint16_t* Vs = Ks + KTILE;
+
+      // S^T = K Q^T
+      f32x16 sacc[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        sacc[kb] = f32x16{};
+        const uint16_t* kp = Ks + (kb * 32 + krow) * KLD + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) sacc[kb] = mfma32<E>(ld16(kp + 16 * s), qf[s], sacc[kb]);
+      }
+
+      // scale, mask, online softmax (log2 domain)
+      float sc[KB], vs[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if constexpr (KV::bytes == 1) {
+          const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
+          sc[kb] = a.qk_scale * ksc[blk];
+          vs[kb] = vsc[blk];
+        } else {
+          sc[kb] = a.qk_scale;
+          vs[kb] = 1.f;
+        }
+      }
+      const bool need_mask = n0 + BN > mask_from;
+      float mt = NEG_INF;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = sacc[kb][r] * sc[kb];
+          if (need_mask) {
+            const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+            const bool ok = n < khi && (!a.causal || n <= qi + offset);
+            x = ok ? x : NEG_INF;
+          }
+          sacc[kb][r] = x;
+          mt = fmaxf(mt, x);
+        }
+      }
+      mt = max_xor32(mt);
+      const float m_new = fmaxf(m_run, mt);
+      const float m_safe = (m_new == NEG_INF) ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - m_safe);
+      float rs = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = fast_exp2(sacc[kb][r] - m_safe);
+          sacc[kb][r] = p;
+          rs += p;
+        }
+      }
+      l_run = l_run * alpha + rs;
+      m_run = m_new;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+
+      // P^T as 16-bit B operands (v_scale folded in for FP8 K/V)
+      u32x4 pf[KB][2];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float v = vs[kb];
+          pf[kb][h] = u32x4{pack2<E>(sacc[kb][8 * h + 0] * v, sacc[kb][8 * h + 1] * v),
+                            pack2<E>(sacc[kb][8 * h + 2] * v, sacc[kb][8 * h + 3] * v),
+                            pack2<E>(sacc[kb][8 * h + 4] * v, sacc[kb][8 * h + 5] * v),
+                            pack2<E>(sacc[kb][8 * h + 6] * v, sacc[kb][8 * h + 7] * v)};
+        }
+      }
+
+      // O^T += V^T P^T
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint16_t* vp = Vs + (kb * 32 + 16 * h) * VLD + d * 32 + tr_off;
+            const u32x2 lo = lds_read_tr16(vp);
+            const u32x2 hi = lds_read_tr16(vp + 4 * VLD);
+            oacc[d] = mfma32<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf[kb][h], oacc[d]);
+          }
+        }
+      }
+    }
+
+    if (t + 1 < n_tiles) lstore((t + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----------------------------------------------------------------------
+  if (!wave_active) return;
+  const float l_tot = sum_xor32(l_run);  // each lane summed its 16 of the row's keys per tile
+  if (!row_ok) return;
+  if constexpr (!SPLIT) {
+    // Rows that saw no key have l == 0 and emit zeros (triton_fwd.py:163-165).
+    const float l_safe = (l_tot == 0.f) ? 1.f : l_tot;
+    const float inv = 1.f / l_safe;
+    uint16_t* op = (uint16_t*)a.o + (int64_t)b * a.sob + (int64_t)hq * a.soh + (qtok0 + qi) * a.son;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = d * 32 + 8 * rq + 4 * g;
+        st8(op + d0, u32x2{pack2<E>(oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv),
+                           pack2<E>(oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv)});
+      }
+    }
+    if (a.lse != nullptr && g == 0) {
+      // natural-log LSE (triton_fwd.py:169-172)
+      a.lse[(int64_t)b * a.slb + (int64_t)hq * a.slh + qi] = (m_run + __log2f(l_safe)) * kLn2;
+    }
+  } else {
+    // un-normalised partial + log2-domain statistics (triton_splitk.py:90-96)
+    const int64_t prow = ((int64_t)(b * a.hq + hq) * seq_q + qi) * a.n_split + split;
+    float* op = (float*)a.o + prow * D;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = d * 32 + 8 * rq + 4 * g;
+        st16(op + d0, __builtin_bit_cast(u32x4, f32x4{oacc[d][4 * rq], oacc[d][4 * rq + 1], oacc[d][4 * rq + 2],
+                                                      oacc[d][4 * rq + 3]}));
+      }
+    }
+    if (g == 0) st8(a.ml + prow * 2, __builtin_bit_cast(u32x2, f32x2{m_run, l_tot}));
+  }
+}
+
+// Log-sum-exp merge of split-K partials (triton_splitk.py:99-127):
+//   m = max_s m_s;  w_s = 2^(m_s - m);  O = sum_s w_s O_s / sum_s w_s l_s   (0 when the sum is 0)
+// One 256-thread workgroup per output row; D/4 threads cover a partial row with
+// float4 loads, so 256/(D/4) splits are read concurrently.
+template <int D, class E>
+__global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c) {
+  constexpr int TPS = D / 4;
+  constexpr int SPB = 256 / TPS;
+  constexpr float NEG_INF = -__builtin_inff();
+  __shared__ float red[256];
+  __shared__ f32x4 part[SPB][TPS];
+  __shared__ float lpart[SPB];
+
+  const int64_t row = blockIdx.x;  // (b, hq, qi) flattened
+  const int S = c.n_split;
+  const float* ml = c.ml + row * S * 2;
+  const float* op = c.opart + row * (int64_t)S * D;
+  const int tid = (int)threadIdx.x;
+
+  float m = NEG_INF;
+  for (int s = tid; s < S; s += 256) m = fmaxf(m, ml[2 * s]);
+  red[tid] = m;
+  __syncthreads();
+#pragma unroll
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+    __syncthreads();
+  }
+  const float mx = red[0];
+  const float m_safe = (mx == NEG_INF) ? 0.f : mx;
+
+  const int sg = tid / TPS, dq = tid % TPS;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+#pragma unroll 4
+  for (int s = sg; s < S; s += SPB) {
+    const f32x2 st = __builtin_bit_cast(f32x2, ld8(ml + 2 * s));
+    const float w = fast_exp2(st[0] - m_safe);
+    l += w * st[1];
+    acc += w * __builtin_bit_cast(f32x4, ld16(op + (int64_t)s * D + 4 * dq));
+  }
+  part[sg][dq] = acc;
+  if (dq == 0) lpart[sg] = l;
+  __syncthreads();
+  if (tid < TPS) {
+    f32x4 tot = part[0][tid];
+    float lt = lpart[0];
+#pragma unroll
+    for (int k = 1; k < SPB; ++k) {
+      tot += part[k][tid];
+      lt += lpart[k];
+    }
+    const float inv = 1.f / ((lt == 0.f) ? 1.f : lt);
+    const int qi = (int)(row % c.nq);
+    const int64_t bh = row / c.nq;
+    const int hq = (int)(bh % c.hq);
+    const int64_t b = bh / c.hq;
+    uint16_t* o = (uint16_t*)c.o + b * c.sob + (int64_t)hq * c.soh + (int64_t)qi * c.son + 4 * tid;
+    st8(o, u32x2{pack2<E>(tot[0] * inv, tot[1] * inv), pack2<E>(tot[2] * inv, tot[3] * inv)});
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Host-side launchers
+// ------------------------------------------------------------------------------------
+
+template <int D, class E, class KV, int NW, int BN, bool SPLIT>
+static hipError_t launch_tile(const TileArgs& a, hipStream_t stream) {
+  constexpr size_t lds = TileShape<D, BN, KV::bytes>::LDS_BYTES;
+  auto kern = attn_tile_kernel<D, E, KV, NW, BN, SPLIT>;
+  static const hipError_t attr_status =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr_status != hipSuccess) return attr_status;
+  hipLaunchKernelGGL(kern, dim3((unsigned)a.total), dim3(NW * 64), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int D, class E>
+static hipError_t launch_combine(const CombineArgs& c, int64_t rows, hipStream_t stream) {
+  hipLaunchKernelGGL((splitk_combine_kernel<D, E>), dim3((unsigned)rows), dim3(256), 0, stream, c);
+  return hipGetLastError();
+}
+
+static fa_status hip_status(hipError_t e, const char** err) {
+  if (e == hipSuccess) return FA_OK;
+  *err = hipGetErrorString(e);
+  return FA_ERR_HIP;
+}
+
+static TileArgs common_args(const fa_fwd_params& p) {
+  TileArgs a{};
+  a.q = p.q;
+  a.k = p.k;
+  a.v = p.v;
+  a.sqb = p.q_stride_b;
+  a.sqh = p.q_stride_h;
+  a.sqn = p.q_stride_n;
+  a.skb = p.k_stride_b;
+  a.skh = p.k_stride_h;
+  a.skn = p.k_stride_n;
+  a.svb = p.v_stride_b;
+  a.svh = p.v_stride_h;
+  a.svn = p.v_stride_n;
+  a.hq = p.heads_q;
+  a.hkv = p.heads_kv;
+  a.group = p.heads_q / p.heads_kv;
+  a.nq = p.seqlen_q;
+  a.nk = p.seqlen_k;
+  a.qk_scale = p.scale * kLog2e;  // same fp32 product as triton_fwd.py:143
+  a.causal = p.causal ? 1 : 0;
+  a.k_scale = p.k_scale;
+  a.v_scale = p.v_scale;
+  a.ssb = p.scale_stride_b;
+  a.ssh = p.scale_stride_h;
+  return a;
+}
+
+fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
+  constexpr int NW = 4, BN = 64;
+  TileArgs a = common_args(p);
+  a.o = p.o;
+  a.sob = p.o_stride_b;
+  a.soh = p.o_stride_h;
+  a.son = p.o_stride_n;
+  a.lse = p.lse;
+  a.slb = p.lse_stride_b;
+  a.slh = p.lse_stride_h;
+  a.varlen = varlen ? 1 : 0;
+  if (varlen) {
+    a.cu_q = p.cu_seqlens_q;
+    a.cu_k = p.cu_seqlens_k;
+    a.nq = p.max_seqlen_q;
+    a.nk = p.max_seqlen_k;
+    a.sqb = a.skb = a.svb = a.sob = 0;
+  }
+  if (a.nq <= 0 || p.batch <= 0) return FA_OK;
+  a.n_rowblk = (a.nq + NW * 32 - 1) / (NW * 32);
+  const int64_t total = (int64_t)p.batch * p.heads_q * a.n_rowblk;
+  if (total > INT32_MAX) {
+    *err = "grid too large";
+    return FA_ERR_UNSUPPORTED;
+  }
+  a.total = (int32_t)total;
+  a.n_split = 1;
+  a.split_len = 0;
+  hipError_t e = hipErrorInvalidValue;
+  const bool bf = p.dtype == FA_DTYPE_BF16;
+  if (p.head_dim == 128) {
+    e = bf ? launch_tile<128, BF16, BF16, NW, BN, false>(a, stream) : launch_tile<128, F16, F16, NW, BN, false>(a, stream);
+  } else if (p.head_dim == 64) {
+    e = bf ? launch_tile<64, BF16, BF16, NW, BN, false>(a, stream) : launch_tile<64, F16, F16, NW, BN, false>(a, stream);
+  }
+  return hip_status(e, err);
+}
+
+int splitk_waves_for_rows(int rows) { return rows <= 32 ? 1 : (rows <= 64 ? 2 : 4); }
+
+template <int D, class E, class KV>
+static hipError_t launch_split_nw(const TileArgs& a, int nw, hipStream_t stream) {
+  switch (nw) {
+    case 1:
+      return launch_tile<D, E, KV, 1, 32, true>(a, stream);
+    case 2:
+      return launch_tile<D, E, KV, 2, 64, true>(a, stream);
+    default:
+      return launch_tile<D, E, KV, 4, 64, true>(a, stream);
+  }
+}
+
+template <int D, class E>
+static hipError_t launch_split(const TileArgs& a, bool fp8, int nw, hipStream_t stream) {
+  return fp8 ? launch_split_nw<D, E, FP8>(a, nw, stream) : launch_split_nw<D, E, E>(a, nw, stream);
+}
+
+fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,
+                     const char** err) {
+  TileArgs a = common_args(p);
+  if (p.batch <= 0 || p.seqlen_q <= 0) return FA_OK;
+  const int S = p.seqlen_k > 0 ? (p.seqlen_k + split_len - 1) / split_len : 1;
+  const int rows = a.group * p.seqlen_q;
+  const int nw = splitk_waves_for_rows(rows);
+  a.n_rowblk = (rows + nw * 32 - 1) / (nw * 32);
+  a.n_split = S;
+  a.split_len = split_len;
+  const int64_t total = (int64_t)p.batch * p.heads_kv * S * a.n_rowblk;
+  const int64_t out_rows = (int64_t)p.batch * p.heads_q * p.seqlen_q;
+  if (total > INT32_MAX || out_rows > INT32_MAX) {
+    *err = "grid too large";
+    return FA_ERR_UNSUPPORTED;
+  }
+  a.total = (int32_t)total;
+  a.o = workspace;
+  a.ml = (float*)workspace + out_rows * S * p.head_dim;
+  const bool fp8 = p.kv_dtype == FA_DTYPE_FP8_E4M3;
+  const bool bf = p.dtype == FA_DTYPE_BF16;
+  hipError_t e = hipErrorInvalidValue;
+  if (p.head_dim == 128) {
+    e = bf ? launch_split<128, BF16>(a, fp8, nw, stream) : launch_split<128, F16>(a, fp8, nw, stream);
+  } else if (p.head_dim == 64) {
+    e = bf ? launch_split<64, BF16>(a, fp8, nw, stream) : launch_split<64, F16>(a, fp8, nw, stream);
+  }
+  if (e != hipSuccess) return hip_status(e, err);
+
+  CombineArgs c{};
+  c.opart = (const float*)a.o;
+  c.ml = a.ml;
+  c.o = p.o;
+  c.sob = p.o_stride_b;
+  c.soh = p.o_stride_h;
+  c.son = p.o_stride_n;
+  c.hq = p.heads_q;
+  c.nq = p.seqlen_q;
+  c.n_split = S;
+  if (p.head_dim == 128) {
+    e = bf ? launch_combine<128, BF16>(c, out_rows, stream) : launch_combine<128, F16>(c, out_rows, stream);
+  } else {
+    e = bf ? launch_combine<64, BF16>(c, out_rows, stream) : launch_combine<64, F16>(c, out_rows, stream);
+  }
+  return hip_status(e, err);
+}
+
+}  // namespace fa

@@ -1,0 +1,369 @@
+"""ctypes binding of ``libfused_attn_hip.so`` (the C ABI in ``include/fused_attn_hip.h``).
+
+This module replaces the reference's compiled pybind extension ``fused_attn._C``
+(csrc/bindings.cpp:90-96).  It turns torch tensors into the plain pointers,
+element strides and sizes of ``fa_fwd_params``, allocates every output and
+workspace with the torch caching allocator on the tensors' device, enqueues the
+kernels on the current stream and maps ``fa_status`` codes to ``RuntimeError``
+(the reference's TORCH_CHECK failures surfaced as RuntimeError too,
+csrc/bindings.cpp:35-50).
+
+There is no fallback here: if the library is missing or the device is not a
+gfx950 GPU, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import threading
+from typing import Optional
+
+import torch
+
+LIB_NAME = "libfused_attn_hip.so"
+ABI_VERSION = 1
+
+# fa_dtype codes
+F16, BF16, F32, FP8_E4M3 = 0, 1, 2, 3
+_DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+_FP8 = getattr(torch, "float8_e4m3fn", None)
+if _FP8 is not None:
+    _DTYPE_CODE[_FP8] = FP8_E4M3
+
+FA_OK, FA_ERR_INVALID_ARGUMENT, FA_ERR_UNSUPPORTED, FA_ERR_WORKSPACE, FA_ERR_HIP = range(5)
+_STATUS_NAME = {
+    FA_ERR_INVALID_ARGUMENT: "invalid argument",
+    FA_ERR_UNSUPPORTED: "unsupported",
+    FA_ERR_WORKSPACE: "workspace",
+    FA_ERR_HIP: "HIP error",
+}
+
+HEAD_DIMS = (64, 128)
+DTYPES = (torch.float16, torch.bfloat16)
+FP8_QBLOCK = 64  # keys per FP8 scale block; split-K partitions are multiples of it
+
+
+class FwdParams(ctypes.Structure):
+    """Mirror of ``fa_fwd_params`` (include/fused_attn_hip.h)."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("q_stride_b", ctypes.c_int64),
+        ("q_stride_h", ctypes.c_int64),
+        ("q_stride_n", ctypes.c_int64),
+        ("k_stride_b", ctypes.c_int64),
+        ("k_stride_h", ctypes.c_int64),
+        ("k_stride_n", ctypes.c_int64),
+        ("v_stride_b", ctypes.c_int64),
+        ("v_stride_h", ctypes.c_int64),
+        ("v_stride_n", ctypes.c_int64),
+        ("o_stride_b", ctypes.c_int64),
+        ("o_stride_h", ctypes.c_int64),
+        ("o_stride_n", ctypes.c_int64),
+        ("batch", ctypes.c_int32),
+        ("heads_q", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32),
+        ("seqlen_q", ctypes.c_int32),
+        ("seqlen_k", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("causal", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("cu_seqlens_q", ctypes.c_void_p),
+        ("cu_seqlens_k", ctypes.c_void_p),
+        ("max_seqlen_q", ctypes.c_int32),
+        ("max_seqlen_k", ctypes.c_int32),
+        ("lse", ctypes.c_void_p),
+        ("lse_stride_b", ctypes.c_int64),
+        ("lse_stride_h", ctypes.c_int64),
+        ("k_scale", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
+        ("scale_stride_b", ctypes.c_int64),
+        ("scale_stride_h", ctypes.c_int64),
+    ]
+
+
+_lib = None
+_lib_error: Optional[str] = None
+_lock = threading.Lock()
+
+
+def library_path() -> str:
+    """``$FUSED_ATTN_HIP_LIB`` if set, else the in-tree build next to this file."""
+    return os.environ.get("FUSED_ATTN_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+
+def _bind(lib: ctypes.CDLL) -> None:
+    P = ctypes.POINTER(FwdParams)
+    lib.fa_attention_fwd.argtypes = [P, ctypes.c_void_p]
+    lib.fa_attention_fwd.restype = ctypes.c_int
+    lib.fa_attention_varlen_fwd.argtypes = [P, ctypes.c_void_p]
+    lib.fa_attention_varlen_fwd.restype = ctypes.c_int
+    lib.fa_splitk_workspace_bytes.argtypes = [ctypes.c_int32] * 5
+    lib.fa_splitk_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_attention_splitk.argtypes = [P, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.fa_attention_splitk.restype = ctypes.c_int
+    lib.fa_choose_num_splits.argtypes = [ctypes.c_int32] * 5
+    lib.fa_choose_num_splits.restype = ctypes.c_int32
+    lib.fa_device_supported.argtypes = [ctypes.c_int32]
+    lib.fa_device_supported.restype = ctypes.c_int32
+    lib.fa_last_error.argtypes = []
+    lib.fa_last_error.restype = ctypes.c_char_p
+    lib.fa_abi_version.argtypes = []
+    lib.fa_abi_version.restype = ctypes.c_int32
+
+
+def load_library() -> ctypes.CDLL:
+    """Load and bind the shared library once; raise RuntimeError if it is unusable."""
+    global _lib, _lib_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not os.path.exists(path):
+            _lib_error = f"{path} not found: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+            raise RuntimeError(f"fused_attn HIP backend unavailable: {_lib_error}")
+        try:
+            lib = ctypes.CDLL(path)
+            _bind(lib)
+        except OSError as e:
+            _lib_error = str(e)
+            raise RuntimeError(f"fused_attn HIP backend unavailable: {e}") from e
+        got = lib.fa_abi_version()
+        if got != ABI_VERSION:
+            _lib_error = f"ABI version mismatch: library {got}, bindings {ABI_VERSION}"
+            raise RuntimeError(f"fused_attn HIP backend unavailable: {_lib_error}")
+        _lib = lib
+        return lib
+
+
+def library_loaded() -> bool:
+    try:
+        load_library()
+        return True
+    except RuntimeError:
+        return False
+
+
+_device_ok: dict[int, bool] = {}
+
+
+def device_supported(device: torch.device | int | None = None) -> bool:
+    """True when the library loads and ``device`` is a gfx950 GPU (has_tensor_core_kernel analogue)."""
+    if not torch.cuda.is_available():
+        return False
+    if device is None:
+        idx = torch.cuda.current_device()
+    elif isinstance(device, int):
+        idx = device
+    else:
+        idx = torch.device(device).index
+        idx = torch.cuda.current_device() if idx is None else idx
+    if idx not in _device_ok:
+        try:
+            _device_ok[idx] = bool(load_library().fa_device_supported(idx))
+        except RuntimeError:
+            _device_ok[idx] = False
+    return _device_ok[idx]
+
+
+def available() -> bool:
+    return device_supported()
+
+
+def _check(status: int, what: str) -> None:
+    if status != FA_OK:
+        msg = load_library().fa_last_error().decode(errors="replace")
+        raise RuntimeError(f"fused_attn HIP {what} failed ({_STATUS_NAME.get(status, status)}): {msg}")
+
+
+# ----------------------------------------------------------------------------------------------
+# tensor preparation
+# ----------------------------------------------------------------------------------------------
+
+
+def _aligned_view(t: torch.Tensor, vec_elems: int, base_align: int) -> torch.Tensor:
+    """``t`` itself when its D stride is 1 and its pointer/other strides allow the kernels'
+    vector accesses, else a contiguous copy (the kernels never see an unaligned view)."""
+    ok = t.stride(-1) == 1 and t.data_ptr() % base_align == 0
+    if ok:
+        for i in range(t.dim() - 1):
+            if t.size(i) > 1 and t.stride(i) % vec_elems != 0:
+                ok = False
+                break
+    # clone, not contiguous(): an already-contiguous view at an unaligned offset must be copied too
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
+
+
+def _prep_qkv(q, k, v, kv_fp8: bool = False):
+    q = _aligned_view(q, 8, 16)
+    kv_vec = 16 if kv_fp8 else 8
+    k = _aligned_view(k, kv_vec, 16)
+    v = _aligned_view(v, kv_vec, 16)
+    return q, k, v
+
+
+def _new_output(q: torch.Tensor) -> torch.Tensor:
+    # empty_like keeps q's strides when q is dense (e.g. a [B,N,H,D] transpose view), as
+    # torch::empty_like does in the reference (csrc/bindings.cpp:56).
+    o = torch.empty_like(q)
+    if o.stride(-1) != 1 or any(o.size(i) > 1 and o.stride(i) % 4 for i in range(o.dim() - 1)):
+        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    return o
+
+
+def _stride(t: torch.Tensor, i: int) -> int:
+    # a size-1 dim is never stepped over; its stride is irrelevant and passed as 0
+    return t.stride(i) if t.size(i) > 1 else 0
+
+
+def make_params(q, k, v, o, causal: bool, scale: float, *, kv_dtype=None, lse=None, k_scale=None, v_scale=None,
+                cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0) -> FwdParams:
+    """Fill ``fa_fwd_params`` from tensors.  Dense: q/o [B,Hq,Nq,D], k/v [B,Hkv,Nk,D].
+    Varlen: q/o [Tq,Hq,D], k/v [Tk,Hkv,D] with int32 cu_seqlens of length batch+1."""
+    p = FwdParams()
+    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    if cu_seqlens_q is None:
+        p.q_stride_b, p.q_stride_h, p.q_stride_n = _stride(q, 0), _stride(q, 1), _stride(q, 2)
+        p.k_stride_b, p.k_stride_h, p.k_stride_n = _stride(k, 0), _stride(k, 1), _stride(k, 2)
+        p.v_stride_b, p.v_stride_h, p.v_stride_n = _stride(v, 0), _stride(v, 1), _stride(v, 2)
+        p.o_stride_b, p.o_stride_h, p.o_stride_n = _stride(o, 0), _stride(o, 1), _stride(o, 2)
+        p.batch, p.heads_q, p.seqlen_q, p.head_dim = q.shape
+        p.heads_kv, p.seqlen_k = k.shape[1], k.shape[2]
+    else:
+        p.q_stride_b = p.k_stride_b = p.v_stride_b = p.o_stride_b = 0
+        p.q_stride_h, p.q_stride_n = _stride(q, 1), _stride(q, 0)
+        p.k_stride_h, p.k_stride_n = _stride(k, 1), _stride(k, 0)
+        p.v_stride_h, p.v_stride_n = _stride(v, 1), _stride(v, 0)
+        p.o_stride_h, p.o_stride_n = _stride(o, 1), _stride(o, 0)
+        p.batch = cu_seqlens_q.numel() - 1
+        p.heads_q, p.head_dim = q.shape[1], q.shape[2]
+        p.heads_kv = k.shape[1]
+        p.seqlen_q, p.seqlen_k = int(max_seqlen_q), int(max_seqlen_k)
+        p.cu_seqlens_q, p.cu_seqlens_k = cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr()
+        p.max_seqlen_q, p.max_seqlen_k = int(max_seqlen_q), int(max_seqlen_k)
+    p.scale = float(scale)
+    p.causal = 1 if causal else 0
+    p.dtype = _DTYPE_CODE.get(q.dtype, -1)
+    p.kv_dtype = _DTYPE_CODE.get(k.dtype if kv_dtype is None else kv_dtype, -1)
+    if lse is not None:
+        p.lse = lse.data_ptr()
+        p.lse_stride_b, p.lse_stride_h = lse.stride(0), lse.stride(1)
+    if k_scale is not None:
+        p.k_scale, p.v_scale = k_scale.data_ptr(), v_scale.data_ptr()
+        p.scale_stride_b, p.scale_stride_h = k_scale.stride(0), k_scale.stride(1)
+    return p
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise RuntimeError("fused_attn HIP backend needs GPU tensors")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"all tensors must be on {dev}, got {t.device}")
+    if not device_supported(dev):
+        raise RuntimeError(
+            f"fused_attn HIP backend unavailable on {dev}: "
+            + (_lib_error or "device is not a gfx950 GPU (set FUSED_ATTN_BACKEND=reference to run the unfused path)"))
+
+
+def supports(q: torch.Tensor, k: torch.Tensor) -> bool:
+    """Shapes/dtypes the MFMA kernels implement (the mma kernel's checks, csrc/bindings.cpp:39-43)."""
+    return (q.dtype in DTYPES and k.dtype in (q.dtype, _FP8) and q.shape[-1] in HEAD_DIMS
+            and q.shape[-1] == k.shape[-1])
+
+
+# ----------------------------------------------------------------------------------------------
+# entry points
+# ----------------------------------------------------------------------------------------------
+
+
+def fwd(q, k, v, causal: bool = False, scale: Optional[float] = None, return_lse: bool = False,
+        out: Optional[torch.Tensor] = None):
+    """Dense FA2 forward.  q [B,Hq,Nq,D]; k, v [B,Hkv,Nk,D]; returns o (and natural-log LSE [B,Hq,Nq])."""
+    _require_gpu(q, k, v)
+    lib = load_library()
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    q, k, v = _prep_qkv(q, k, v)
+    o = _new_output(q) if out is None else out
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if return_lse else None
+    p = make_params(q, k, v, o, causal, scale, lse=lse)
+    with torch.cuda.device(q.device):
+        _check(lib.fa_attention_fwd(ctypes.byref(p), ctypes.c_void_p(_stream(q))), "attention_fwd")
+    return (o, lse) if return_lse else o
+
+
+def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int, causal: bool = False,
+               scale: Optional[float] = None, out: Optional[torch.Tensor] = None):
+    """Packed varlen forward.  q [Tq,Hq,D]; k, v [Tk,Hkv,D]; cu_seqlens int32 [nseq+1] on the GPU."""
+    _require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k)
+    if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
+        raise RuntimeError("cu_seqlens must be int32")
+    if cu_seqlens_q.numel() != cu_seqlens_k.numel():
+        raise RuntimeError("cu_seqlens_q and cu_seqlens_k must have the same length")
+    lib = load_library()
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    q, k, v = _prep_qkv(q, k, v)
+    cu_q, cu_k = cu_seqlens_q.contiguous(), cu_seqlens_k.contiguous()
+    o = _new_output(q) if out is None else out
+    p = make_params(q, k, v, o, causal, scale, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=max_seqlen_q,
+                    max_seqlen_k=max_seqlen_k)
+    with torch.cuda.device(q.device):
+        _check(lib.fa_attention_varlen_fwd(ctypes.byref(p), ctypes.c_void_p(_stream(q))), "attention_varlen_fwd")
+    return o
+
+
+def split_len_for(seqlen_k: int, num_splits: int, block: int = FP8_QBLOCK) -> int:
+    """Split length rounded up to whole ``block``-key tiles (triton_splitk.py:153-154)."""
+    num_splits = max(1, int(num_splits))
+    per = -(-max(seqlen_k, 1) // num_splits)
+    return -(-per // block) * block
+
+
+def splitk(q, k, v, causal: bool = False, scale: Optional[float] = None, split_len: int = 128,
+           k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None):
+    """Split-K flash-decoding + LSE combine.  k/v may be float8_e4m3fn with per-64-key fp32 scales."""
+    _require_gpu(q, k, v)
+    lib = load_library()
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    fp8 = _FP8 is not None and k.dtype == _FP8
+    q, k, v = _prep_qkv(q, k, v, kv_fp8=fp8)
+    if fp8:
+        k_scale = k_scale.float().contiguous() if k_scale.stride(-1) != 1 else k_scale
+        v_scale = v_scale.float().contiguous() if v_scale.stride(-1) != 1 else v_scale
+        if k_scale.stride() != v_scale.stride():
+            k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()
+    o = _new_output(q)
+    b, hq, nq, d = q.shape
+    nk = k.shape[2]
+    splits = -(-nk // split_len) if nk > 0 else 1
+    need = lib.fa_splitk_workspace_bytes(b, hq, nq, d, splits)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=q.device)
+    p = make_params(q, k, v, o, causal, scale, k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None)
+    with torch.cuda.device(q.device):
+        _check(lib.fa_attention_splitk(ctypes.byref(p), int(split_len), ctypes.c_void_p(workspace.data_ptr()),
+                                       workspace.numel() * workspace.element_size(),
+                                       ctypes.c_void_p(_stream(q))), "attention_splitk")
+    return o
+
+
+def choose_num_splits(batch: int, heads: int, seqlen_k: int, seqlen_q: int, num_cus: int) -> int:
+    return int(load_library().fa_choose_num_splits(batch, heads, seqlen_k, seqlen_q, num_cus))
+
+
+def workspace_bytes(batch: int, heads_q: int, seqlen_q: int, head_dim: int, num_splits: int) -> int:
+    return int(load_library().fa_splitk_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits))

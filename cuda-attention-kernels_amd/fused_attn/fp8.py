@@ -1,0 +1,86 @@
+"""FP8 (OCP E4M3, ``torch.float8_e4m3fn``) KV cache.
+
+Decode is bound by reading K/V, so an FP8 cache halves the bytes streamed from
+HBM.  Values are scaled per (batch, kv-head, block of ``QBLOCK`` keys): each
+block is divided by absmax/448 before the cast (fused_attn/fp8.py:26-45).
+
+    k8, ks = quantize_kv_fp8(k)          # [B,Hkv,N,D] float8_e4m3fn, [B,Hkv,ceil(N/64)] fp32
+    v8, vs = quantize_kv_fp8(v)
+    o = attention_fp8(q, k8, ks, v8, vs, causal=True)
+
+The quantiser and dequantiser are torch op chains in the reference's order, so
+their bits equal the reference's on the same torch.  ``attention_fp8`` runs the
+HIP split-K kernel, which converts each E4M3 element exactly to q's 16-bit type
+as it stages K/V through LDS, multiplies the score block by
+``scale * k_scale`` and folds ``v_scale`` into P before the PV product.  Any
+number of queries is accepted (prefill-shaped calls too).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _hip
+from .reference import attention_reference
+
+QBLOCK = 64  # keys per scale
+E4M3_MAX = 448.0
+FP8_DTYPE = getattr(torch, "float8_e4m3fn", None)
+
+
+def quantize_kv_fp8(x: torch.Tensor, qblock: int = QBLOCK) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [B, Hkv, N, D] (any float dtype) -> (float8_e4m3fn, same shape; fp32 scales [B, Hkv, ceil(N/qblock)])."""
+    assert FP8_DTYPE is not None, "this torch build has no float8_e4m3fn"
+    b, h, n, d = x.shape
+    nblk = -(-n // qblock)
+    xf = x.float()
+    pad = nblk * qblock - n
+    if pad:
+        xf = torch.nn.functional.pad(xf, (0, 0, 0, pad))
+    blocks = xf.view(b, h, nblk, qblock, d)
+    scale = blocks.abs().amax(dim=(-1, -2)).clamp_min(1e-12) / E4M3_MAX  # [B, Hkv, nblk]
+    scaled = (blocks / scale[..., None, None]).clamp(-E4M3_MAX, E4M3_MAX)
+    x8 = scaled.to(FP8_DTYPE).view(b, h, nblk * qblock, d)[:, :, :n].contiguous()
+    return x8, scale.contiguous()
+
+
+def dequantize_kv_fp8(x8: torch.Tensor, scale: torch.Tensor, qblock: int = QBLOCK) -> torch.Tensor:
+    """Inverse of ``quantize_kv_fp8`` up to rounding: fp32 [B, Hkv, N, D] (fused_attn/fp8.py:48-56)."""
+    b, h, n, d = x8.shape
+    nblk = scale.shape[-1]
+    xf = x8.float()
+    pad = nblk * qblock - n
+    if pad:
+        xf = torch.nn.functional.pad(xf, (0, 0, 0, pad))
+    out = xf.view(b, h, nblk, qblock, d) * scale[..., None, None]
+    return out.view(b, h, nblk * qblock, d)[:, :, :n]
+
+
+def attention_fp8(
+    q: torch.Tensor,
+    k8: torch.Tensor,
+    k_scale: torch.Tensor,
+    v8: torch.Tensor,
+    v_scale: torch.Tensor,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    split_len: Optional[int] = None,
+) -> torch.Tensor:
+    """Attention over an FP8 K/V cache (reference signature: fused_attn/fp8.py:125-128, plus ``split_len``)."""
+    assert q.dtype in (torch.float16, torch.bfloat16), \
+        "Q must be fp16/bf16 (FP8 is converted to Q's dtype for the MFMA)"
+    assert k8.dtype == FP8_DTYPE and v8.dtype == FP8_DTYPE
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    if not q.is_cuda:
+        return attention_reference(q, dequantize_kv_fp8(k8, k_scale), dequantize_kv_fp8(v8, v_scale),
+                                   causal=causal, scale=scale)
+    if split_len is None:
+        split_len = 128 if q.shape[-2] <= 16 else max(QBLOCK, -(-k8.shape[-2] // QBLOCK) * QBLOCK)
+    return _hip.splitk(q, k8, v8, causal=causal, scale=scale, split_len=int(split_len), k_scale=k_scale,
+                       v_scale=v_scale)
+
+
+# The reference exported the Triton entry under this name (fused_attn/__init__.py:5-9).
+attention_fp8_triton = attention_fp8

@@ -1,0 +1,139 @@
+"""Public op and backend dispatch.
+
+``fused_attn.attention`` is the ``torch.library`` custom op of the reference
+(fused_attn/ops.py:76-104), same name, schema, defaults and fake kernel, so
+``torch.compile(fullgraph=True)`` still traces it and it shows up by name in
+profiler traces.
+
+Dispatch is ``hip`` or ``reference`` (the reference's five backends,
+ops.py:34-73, collapse into these two):
+
+* GPU tensors go to the HIP backend (``_hip``): MFMA FA2 prefill, or split-K
+  flash-decoding for decode-shaped calls (at most 16 queries against at least
+  2048 keys, ops.py:36-37,63-66).  If the HIP library cannot run on the device
+  the call raises; it never falls back silently.
+* CPU tensors, or ``FUSED_ATTN_BACKEND=reference``, use the unfused PyTorch
+  path in ``reference.py``.
+
+``FUSED_ATTN_BACKEND`` also accepts the reference's GPU backend names
+(``cuda_mma``, ``cuda``, ``triton`` -> ``hip``; ``splitk`` -> ``hip`` with the
+split-K kernel forced) so existing environments keep working.
+"""
+from __future__ import annotations
+
+import math
+import os
+from typing import Optional
+
+import torch
+
+from . import _hip
+from .reference import attention_reference, attention_varlen_reference
+
+BACKENDS = ("hip", "reference")
+_ALIASES = {"cuda_mma": "hip", "cuda": "hip", "triton": "hip", "splitk": "hip"}
+SPLITK_MAX_Q = 16  # decode-shaped: few query rows ...
+SPLITK_MIN_K = 2048  # ... against a long context
+DEFAULT_SPLIT_KEYS = 128  # keys per split-K partition (a multiple of 64)
+
+
+def available_backends() -> list[str]:
+    out = []
+    if _hip.available():
+        out.append("hip")
+    out.append("reference")
+    return out
+
+
+def _forced_backend() -> Optional[str]:
+    forced = os.environ.get("FUSED_ATTN_BACKEND")
+    if not forced:
+        return None
+    if forced not in BACKENDS and forced not in _ALIASES:
+        raise ValueError(f"unknown backend {forced!r}; expected one of {BACKENDS} "
+                         f"(or a reference name {tuple(_ALIASES)})")
+    return forced
+
+
+def _pick_backend(q: torch.Tensor, k: Optional[torch.Tensor] = None) -> str:
+    """``hip`` for GPU tensors, ``reference`` otherwise or when forced (reference: ops.py:56-73)."""
+    forced = _forced_backend()
+    if forced is not None:
+        return _ALIASES.get(forced, forced)
+    return "hip" if q.is_cuda else "reference"
+
+
+def is_decode_shaped(q: torch.Tensor, k: Optional[torch.Tensor]) -> bool:
+    """Few queries against a long context: the split-K regime (ops.py:63)."""
+    return k is not None and q.shape[-2] <= SPLITK_MAX_Q and k.shape[-2] >= SPLITK_MIN_K
+
+
+def _hip_kernel_for(q: torch.Tensor, k: torch.Tensor) -> str:
+    """Which HIP kernel family serves this call: ``splitk`` or ``fwd``."""
+    if os.environ.get("FUSED_ATTN_BACKEND") == "splitk" or is_decode_shaped(q, k):
+        return "splitk"
+    return "fwd"
+
+
+@torch.library.custom_op("fused_attn::attention", mutates_args=())
+def attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    scale: Optional[float] = None,
+) -> torch.Tensor:
+    """Fused scaled-dot-product attention.
+
+    q: [B, H_q, N_q, D]; k, v: [B, H_kv, N_k, D] with H_q % H_kv == 0.
+    Returns [B, H_q, N_q, D] in q's dtype.
+    """
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    if _pick_backend(q, k) == "hip":
+        if _hip_kernel_for(q, k) == "splitk":
+            return _hip.splitk(q, k, v, causal=causal, scale=scale,
+                               split_len=default_split_len(q.shape[-2], k.shape[-2]))
+        return _hip.fwd(q, k, v, causal=causal, scale=scale)
+    return attention_reference(q, k, v, causal=causal, scale=scale)
+
+
+@attention.register_fake
+def _attention_fake(q, k, v, causal=False, scale=None):
+    return q.new_empty(q.shape)
+
+
+def default_split_len(seqlen_q: int, seqlen_k: int) -> int:
+    """Keys per split-K partition when the caller does not choose one."""
+    return DEFAULT_SPLIT_KEYS
+
+
+def attention_varlen(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    causal: bool = False,
+    scale: Optional[float] = None,
+) -> torch.Tensor:
+    """Packed/ragged attention. q: [total_q, H_q, D]; k, v: [total_k, H_kv, D] (reference: ops.py:107-124).
+
+    On GPU tensors this runs the HIP kernel in varlen mode (the reference ran its
+    Python reference loop whenever its CUDA extension was built, ops.py:119-124).
+    """
+    if _pick_backend(q) == "hip":
+        return _hip.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, causal=causal,
+                               scale=scale)
+    return attention_varlen_reference(q, k, v, cu_seqlens_q, cu_seqlens_k, causal=causal, scale=scale)
+
+
+def pack_varlen(tensors: list[torch.Tensor]):
+    """[[N_i, H, D], ...] -> (packed [sum N_i, H, D], int32 cu_seqlens [n+1] starting at 0, max N_i)
+    (reference: ops.py:127-132)."""
+    lens = [t.shape[0] for t in tensors]
+    dev = tensors[0].device
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32, device=dev)
+    cu[1:] = torch.cumsum(torch.tensor(lens, device=dev), 0)
+    return torch.cat(tensors, 0), cu, max(lens)

@@ -1,0 +1,136 @@
+/*
+ * fused_attn_hip.h — C ABI of the MI355X (gfx950) fused-attention backend.
+ *
+ * This is the drop-in boundary that replaces the reference's pybind module
+ * `fused_attn._C` (csrc/bindings.cpp:90-96) and its params struct
+ * (csrc/flash_attn.h:9-22), plus the Triton entry points that the reference
+ * reached from Python (fused_attn/triton_fwd.py:225-309,
+ * fused_attn/triton_splitk.py:140-181, fused_attn/fp8.py:125-147).
+ *
+ * Conventions
+ *  - Plain pointers, element strides and sizes; no framework types.
+ *  - All tensor pointers are device pointers on the current HIP device.
+ *  - The caller allocates every buffer (outputs and split-K workspace).  The
+ *    library never allocates device memory and keeps no pointer after return.
+ *  - Every entry point returns an fa_status.  On failure fa_last_error()
+ *    returns a thread-local message.  Nothing throws across this boundary and
+ *    nothing aborts.
+ *  - Work is enqueued on `stream` and is asynchronous, like the reference's
+ *    launches on the current CUDA stream (csrc/bindings.cpp:58,78).
+ */
+#ifndef FUSED_ATTN_HIP_H_
+#define FUSED_ATTN_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+/* Element types (reference: DType, csrc/flash_attn.h:7). */
+typedef enum fa_dtype {
+  FA_DTYPE_F16 = 0,
+  FA_DTYPE_BF16 = 1,
+  FA_DTYPE_F32 = 2,
+  FA_DTYPE_FP8_E4M3 = 3 /* OCP float8_e4m3fn, K/V cache only */
+} fa_dtype;
+
+typedef enum fa_status {
+  FA_OK = 0,
+  FA_ERR_INVALID_ARGUMENT = 1, /* shape / stride / alignment / pointer precondition violated */
+  FA_ERR_UNSUPPORTED = 2,      /* valid request this backend does not implement (dtype, head_dim) */
+  FA_ERR_WORKSPACE = 3,        /* split-K workspace missing or too small */
+  FA_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed */
+} fa_status;
+
+/*
+ * Forward parameters.  Mirrors AttnParams (csrc/flash_attn.h:9-22) with the
+ * varlen, LSE and FP8 fields the Triton paths carried as kernel arguments.
+ *
+ * Dense layout:  q [B, Hq, Nq, D], k/v [B, Hkv, Nk, D], o like q, any strides
+ *                with unit stride along D (strides are in elements).
+ * Varlen layout: q [total_q, Hq, D], k/v [total_k, Hkv, D]; `batch` is the
+ *                number of sequences, cu_seqlens_q/k are device int32 arrays
+ *                of batch+1 prefix offsets starting at 0, the *_stride_b
+ *                fields are ignored and *_stride_n is the token stride.
+ * Head mapping:  q-head h reads kv-head h / (Hq / Hkv) (reference.py:16-21).
+ * Causal:        bottom-right aligned, key j visible to query i iff
+ *                j <= i + (Nk - Nq) (reference.py:24-33); a row with no
+ *                visible key is written as zeros (reference.py:60-61).
+ */
+typedef struct fa_fwd_params {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t q_stride_b, q_stride_h, q_stride_n;
+  int64_t k_stride_b, k_stride_h, k_stride_n;
+  int64_t v_stride_b, v_stride_h, v_stride_n;
+  int64_t o_stride_b, o_stride_h, o_stride_n;
+  int32_t batch, heads_q, heads_kv, seqlen_q, seqlen_k, head_dim;
+  float scale;   /* softmax scale; callers pass 1/sqrt(D) for the default (ops.py:89) */
+  int32_t causal;
+  int32_t dtype;    /* fa_dtype of q and o */
+  int32_t kv_dtype; /* fa_dtype of k and v: equal to dtype, or FA_DTYPE_FP8_E4M3 */
+  /* varlen (NULL for dense) */
+  const int32_t* cu_seqlens_q;
+  const int32_t* cu_seqlens_k;
+  int32_t max_seqlen_q, max_seqlen_k;
+  /* optional natural-log LSE output [B, Hq, Nq] fp32 (NULL = not written);
+     reference: WRITE_LSE in fused_attn/triton_fwd.py:169-172 */
+  float* lse;
+  int64_t lse_stride_b, lse_stride_h;
+  /* FP8 K/V block scales, fp32 [B, Hkv, ceil(Nk/64)] (fused_attn/fp8.py:31-45);
+     used only when kv_dtype == FA_DTYPE_FP8_E4M3 */
+  const float* k_scale;
+  const float* v_scale;
+  int64_t scale_stride_b, scale_stride_h;
+} fa_fwd_params;
+
+/* Dense FA2 forward on MFMA.  Replaces attention_fwd_mma (csrc/bindings.cpp:63-81),
+   run_attention_fwd_mma (csrc/flash_attn.h:27) and attention_triton
+   (fused_attn/triton_fwd.py:225-265).  Supports f16/bf16, D in {64, 128}. */
+fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
+
+/* Packed variable-length forward.  Replaces attention_varlen_triton
+   (fused_attn/triton_fwd.py:268-309).  Needs cu_seqlens_q/k and max_seqlen_q. */
+fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream);
+
+/* Bytes of workspace fa_attention_splitk needs for `num_splits` key partitions:
+   fp32 partial outputs [B, Hq, Nq, S, D] plus (max, sum) pairs [B, Hq, Nq, S, 2]
+   (reference partial buffers: fused_attn/triton_splitk.py:156-158). */
+size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q, int32_t head_dim,
+                                 int32_t num_splits);
+
+/* Split-K flash-decoding: one pass per `split_len`-key partition writing
+   un-normalised fp32 partials and log2-domain statistics, then a
+   log-sum-exp combine kernel.  Replaces attention_splitk_triton
+   (fused_attn/triton_splitk.py:140-181) and, with kv_dtype ==
+   FA_DTYPE_FP8_E4M3 and k_scale/v_scale set, attention_fp8_triton
+   (fused_attn/fp8.py:125-147).  split_len must be a positive multiple of 64;
+   num_splits = ceil(seqlen_k / split_len). */
+fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Reference split heuristic (fused_attn/triton_splitk.py:130-137):
+   min(2*num_cus / (batch*heads), seqlen_k / 256, 64), 1 for seqlen_q > 64. */
+int32_t fa_choose_num_splits(int32_t batch, int32_t heads, int32_t seqlen_k, int32_t seqlen_q, int32_t num_cus);
+
+/* 1 when `device` is a gfx950 GPU this library has kernels for, else 0.
+   Replaces has_tensor_core_kernel (csrc/bindings.cpp:83-86). */
+int32_t fa_device_supported(int32_t device);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* fa_last_error(void);
+
+/* FA_ABI_VERSION of the loaded library. */
+int32_t fa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FUSED_ATTN_HIP_H_ */

@@ -1,0 +1,168 @@
+"""The C ABI library loads, exports every symbol include/fused_attn_hip.h declares, and
+rejects invalid requests with status codes before touching a GPU.  CPU only: no call
+here reaches a kernel launch."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from fused_attn import _hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fused_attn_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_hip.library_path()):
+        pytest.fail(f"{_hip.library_path()} is not built; run __graft_entry__.build()")
+    return _hip.load_library()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = _declared_functions()
+    assert len(names) >= 8
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_struct_layout_matches_header(lib):
+    # fa_fwd_params: 4 pointers, 12 int64 strides, 6 int32 sizes, float, 3 int32,
+    # 2 pointers, 2 int32, pointer + 2 int64, 2 pointers + 2 int64
+    assert ctypes.sizeof(_hip.FwdParams) == 4 * 8 + 12 * 8 + 6 * 4 + 4 + 3 * 4 + 2 * 8 + 2 * 4 + 8 + 16 + 16 + 16
+    assert _hip.FwdParams.cu_seqlens_q.offset % 8 == 0 and _hip.FwdParams.lse.offset % 8 == 0
+
+
+def test_abi_version(lib):
+    assert lib.fa_abi_version() == _hip.ABI_VERSION == 1
+
+
+def test_choose_num_splits_known_answers(lib):
+    assert lib.fa_choose_num_splits(1, 8, 32768, 1, 108) == 27
+    assert lib.fa_choose_num_splits(64, 32, 32768, 1, 108) == 1
+    assert lib.fa_choose_num_splits(1, 1, 512, 1, 108) == 2
+    assert lib.fa_choose_num_splits(1, 1, 100000, 128, 108) == 1
+
+
+def test_workspace_bytes(lib):
+    assert lib.fa_splitk_workspace_bytes(32, 32, 1, 128, 256) == 32 * 32 * 256 * 130 * 4
+    assert lib.fa_splitk_workspace_bytes(0, 32, 1, 128, 256) == 0
+
+
+def _params(**over):
+    p = _hip.FwdParams()
+    # a plausible, aligned dense request; pointers are fake and never dereferenced
+    p.q = p.k = p.v = p.o = 0x10000
+    p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_k, p.head_dim = 1, 4, 2, 16, 16, 64
+    p.q_stride_b, p.q_stride_h, p.q_stride_n = 4 * 16 * 64, 16 * 64, 64
+    p.k_stride_b, p.k_stride_h, p.k_stride_n = 2 * 16 * 64, 16 * 64, 64
+    p.v_stride_b, p.v_stride_h, p.v_stride_n = 2 * 16 * 64, 16 * 64, 64
+    p.o_stride_b, p.o_stride_h, p.o_stride_n = 4 * 16 * 64, 16 * 64, 64
+    p.scale, p.dtype, p.kv_dtype = 0.125, _hip.BF16, _hip.BF16
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(head_dim=96), _hip.FA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(dtype=_hip.F32, kv_dtype=_hip.F32), _hip.FA_ERR_UNSUPPORTED, "dtype"),
+    (dict(heads_q=3), _hip.FA_ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(heads_kv=0), _hip.FA_ERR_INVALID_ARGUMENT, "non-negative"),
+    (dict(kv_dtype=_hip.F16), _hip.FA_ERR_INVALID_ARGUMENT, "k/v dtype"),
+    (dict(kv_dtype=_hip.FP8_E4M3), _hip.FA_ERR_INVALID_ARGUMENT, "k/v dtype"),
+    (dict(q=0x10002), _hip.FA_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(k_stride_n=60), _hip.FA_ERR_INVALID_ARGUMENT, "k/v strides"),
+    (dict(q_stride_h=1020), _hip.FA_ERR_INVALID_ARGUMENT, "q strides"),
+    (dict(o_stride_n=62), _hip.FA_ERR_INVALID_ARGUMENT, "o strides"),
+    (dict(v=0), _hip.FA_ERR_INVALID_ARGUMENT, "non-NULL"),
+    (dict(dtype=9), _hip.FA_ERR_INVALID_ARGUMENT, "unknown dtype"),
+    (dict(scale=float("nan")), _hip.FA_ERR_INVALID_ARGUMENT, "NaN"),
+])
+def test_fwd_validation(lib, over, code, msg):
+    p = _params(**over)
+    assert lib.fa_attention_fwd(ctypes.byref(p), None) == code
+    assert msg in lib.fa_last_error().decode()
+
+
+def test_null_params(lib):
+    assert lib.fa_attention_fwd(None, None) == _hip.FA_ERR_INVALID_ARGUMENT
+    assert lib.fa_attention_varlen_fwd(None, None) == _hip.FA_ERR_INVALID_ARGUMENT
+    assert lib.fa_attention_splitk(None, 128, None, 0, None) == _hip.FA_ERR_INVALID_ARGUMENT
+
+
+def test_empty_requests_succeed_without_launch(lib):
+    assert lib.fa_attention_fwd(ctypes.byref(_params(batch=0)), None) == _hip.FA_OK
+    assert lib.fa_attention_fwd(ctypes.byref(_params(seqlen_q=0)), None) == _hip.FA_OK
+    assert lib.fa_last_error().decode() == ""
+
+
+def test_varlen_validation(lib):
+    p = _params()
+    assert lib.fa_attention_varlen_fwd(ctypes.byref(p), None) == _hip.FA_ERR_INVALID_ARGUMENT
+    assert "cu_seqlens" in lib.fa_last_error().decode()
+    p = _params(cu_seqlens_q=0x20000, cu_seqlens_k=0x20000, max_seqlen_q=-1)
+    assert lib.fa_attention_varlen_fwd(ctypes.byref(p), None) == _hip.FA_ERR_INVALID_ARGUMENT
+    p = _params(cu_seqlens_q=0x20000, cu_seqlens_k=0x20000, max_seqlen_q=8, max_seqlen_k=8, lse=0x30000)
+    assert lib.fa_attention_varlen_fwd(ctypes.byref(p), None) == _hip.FA_ERR_UNSUPPORTED
+
+
+def test_splitk_validation(lib):
+    p = _params()
+    assert lib.fa_attention_splitk(ctypes.byref(p), 100, None, 0, None) == _hip.FA_ERR_INVALID_ARGUMENT
+    assert "multiple of 64" in lib.fa_last_error().decode()
+    assert lib.fa_attention_splitk(ctypes.byref(p), 0, None, 0, None) == _hip.FA_ERR_INVALID_ARGUMENT
+    assert lib.fa_attention_splitk(ctypes.byref(p), 64, None, 0, None) == _hip.FA_ERR_WORKSPACE
+    need = lib.fa_splitk_workspace_bytes(1, 4, 16, 64, 1)
+    assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need - 4,
+                                   None) == _hip.FA_ERR_WORKSPACE
+    assert "need %d" % need in lib.fa_last_error().decode()
+    assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40004), need,
+                                   None) == _hip.FA_ERR_WORKSPACE  # misaligned
+    fp8 = _params(kv_dtype=_hip.FP8_E4M3, k_stride_n=64)
+    assert lib.fa_attention_splitk(ctypes.byref(fp8), 64, ctypes.c_void_p(0x40000), need,
+                                   None) == _hip.FA_ERR_INVALID_ARGUMENT
+    assert "scale" in lib.fa_last_error().decode()
+    fp8 = _params(kv_dtype=_hip.FP8_E4M3, k_stride_n=72, k_scale=0x50000, v_scale=0x50000)
+    assert lib.fa_attention_splitk(ctypes.byref(fp8), 64, ctypes.c_void_p(0x40000), need,
+                                   None) == _hip.FA_ERR_INVALID_ARGUMENT  # fp8 rows need 16-byte strides
+    p = _params(lse=0x30000)
+    assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need, None) == _hip.FA_ERR_UNSUPPORTED
+
+
+def test_make_params_marshals_strides():
+    q = torch.empty(2, 64, 8, 128, dtype=torch.bfloat16).transpose(1, 2)  # [B,H,N,D] view of [B,N,H,D]
+    k = torch.empty(2, 2, 64, 128, dtype=torch.bfloat16)
+    o = torch.empty_like(q)
+    p = _hip.make_params(q, k, k, o, True, 0.5)
+    assert (p.q_stride_b, p.q_stride_h, p.q_stride_n) == (64 * 8 * 128, 128, 8 * 128)
+    assert (p.k_stride_b, p.k_stride_h, p.k_stride_n) == (2 * 64 * 128, 64 * 128, 128)
+    assert (p.o_stride_b, p.o_stride_h, p.o_stride_n) == q.stride()[:3]
+    assert (p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_k, p.head_dim) == (2, 8, 2, 64, 64, 128)
+    assert p.causal == 1 and p.dtype == p.kv_dtype == _hip.BF16 and abs(p.scale - 0.5) < 1e-7
+    # varlen: token stride is dim 0, batch strides unused
+    qv = torch.empty(100, 8, 64, dtype=torch.float16)
+    kv = torch.empty(90, 2, 64, dtype=torch.float16)
+    cu = torch.tensor([0, 40, 100], dtype=torch.int32)
+    p = _hip.make_params(qv, kv, kv, qv, False, 1.0, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=60,
+                         max_seqlen_k=50)
+    assert (p.q_stride_b, p.q_stride_h, p.q_stride_n) == (0, 64, 8 * 64)
+    assert p.batch == 2 and p.max_seqlen_q == 60 and p.seqlen_k == 50 and p.dtype == _hip.F16
+
+
+def test_aligned_view_copies_only_when_needed():
+    t = torch.empty(2, 4, 16, 64, dtype=torch.bfloat16)
+    assert _hip._aligned_view(t, 8, 16) is t
+    odd = torch.randn(4 * 16 * 64 + 1).bfloat16()[1:].view(1, 4, 16, 64)
+    c = _hip._aligned_view(odd, 8, 16)
+    assert c is not odd and c.data_ptr() % 16 == 0 and torch.equal(c, odd)
+    strided = torch.empty(1, 4, 16, 70, dtype=torch.bfloat16)[..., :64]
+    assert _hip._aligned_view(strided, 8, 16).is_contiguous()

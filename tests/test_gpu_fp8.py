@@ -1,0 +1,76 @@
+"""FP8 E4M3 KV-cache attention on the HIP split-K kernel vs the fp32 oracle run on the
+dequantised K/V (reference: tests/test_splitk_fp8.py:77-86)."""
+import pytest
+import torch
+
+import fused_attn
+from helpers import FP8_TOL, announce, max_err, randn
+from oracle import attention_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def test_fp8_kernel_matches_dequantized_oracle_prefill_shaped():
+    """The reference's own GPU case: n_q=128, causal, fp16 q."""
+    announce("fp8 reference case")
+    torch.manual_seed(0)
+    q = randn(2, 8, 128, 64, dtype=torch.float16)
+    k, v = randn(2, 2, 1024, 64), randn(2, 2, 1024, 64)
+    k8, ks = fused_attn.quantize_kv_fp8(k)
+    v8, vs = fused_attn.quantize_kv_fp8(v)
+    out = fused_attn.attention_fp8_triton(q, k8, ks, v8, vs, causal=True)
+    ref = orc.attention_fp8(q.cpu(), k8.cpu(), ks.cpu(), v8.cpu(), vs.cpu(), causal=True)
+    assert out.dtype == q.dtype
+    assert max_err(out, ref) <= FP8_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k,d", [(2, 8, 2, 1, 1000, 128), (1, 4, 4, 3, 4096, 64),
+                                                  (3, 16, 2, 16, 2100, 128), (1, 4, 1, 200, 333, 128)])
+@pytest.mark.parametrize("split_len", [None, 64, 256])
+def test_fp8_matches_oracle(b, h_q, h_kv, n_q, n_k, d, causal, dtype, split_len):
+    announce(f"fp8 b={b} hq={h_q} hkv={h_kv} nq={n_q} nk={n_k} d={d} causal={causal} {dtype} split={split_len}")
+    torch.manual_seed(0)
+    q = randn(b, h_q, n_q, d, dtype=dtype)
+    k, v = randn(b, h_kv, n_k, d), randn(b, h_kv, n_k, d)
+    k8, ks = fused_attn.quantize_kv_fp8(k)
+    v8, vs = fused_attn.quantize_kv_fp8(v)
+    out = fused_attn.attention_fp8(q, k8, ks, v8, vs, causal=causal, split_len=split_len)
+    ref = orc.attention_fp8(q.cpu(), k8.cpu(), ks.cpu(), v8.cpu(), vs.cpu(), causal=causal)
+    assert max_err(out, ref) <= FP8_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fp8_decode_is_exact_for_every_code(dtype):
+    """One key: the output row is exactly the decoded V row times its power-of-two scale.
+    Covers all 254 finite E4M3 codes through the in-kernel conversion."""
+    announce(f"fp8 all codes {dtype}")
+    codes = torch.arange(256, dtype=torch.uint8)
+    codes[codes == 0x7F] = 0
+    codes[codes == 0xFF] = 0
+    v8 = codes.view(torch.float8_e4m3fn).reshape(1, 2, 1, 128).cuda()
+    k8 = torch.zeros_like(v8)
+    ks = torch.ones(1, 2, 1, device="cuda")
+    vs = torch.tensor([[[0.25], [2.0]]], device="cuda")
+    q = randn(1, 2, 1, 128, dtype=dtype)
+    out = fused_attn.attention_fp8(q, k8, ks, v8, vs)
+    want = (v8.float() * vs[..., None]).to(dtype)
+    assert torch.equal(out, want)
+
+
+def test_baseline_fp8_decode_config():
+    """B=16, Hq=64, Hkv=8, n_q=1, n_k=65536, D=128; K/V N(0,1) fp32 quantised per 64-key block."""
+    announce("baseline fp8 decode")
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q = randn(16, 64, 1, 128, dtype=torch.bfloat16, gen=gen)
+    k8, ks = fused_attn.quantize_kv_fp8(randn(16, 8, 65536, 128, gen=gen))
+    v8, vs = fused_attn.quantize_kv_fp8(randn(16, 8, 65536, 128, gen=gen))
+    out = fused_attn.attention_fp8(q, k8, ks, v8, vs, split_len=128)
+    ref = torch.empty(16, 64, 1, 128, device="cuda")
+    for bi in range(16):  # oracle per batch element on the dequantised cache
+        ref[bi:bi + 1] = orc.attention_fp8(q[bi:bi + 1], k8[bi:bi + 1], ks[bi:bi + 1], v8[bi:bi + 1],
+                                           vs[bi:bi + 1])
+    err = max_err(out, ref)
+    print(f"max_abs_err={err:.3e}", flush=True)
+    assert err <= FP8_TOL

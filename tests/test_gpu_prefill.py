@@ -1,0 +1,147 @@
+"""Dense prefill parity: the HIP MFMA kernel (through the public op and the C ABI) vs the fp32 oracle.
+
+Mirrors the reference's kernel tests (tests/test_correctness.py:56-122,
+tests/test_splitk_fp8.py:89-106) at the tolerances this build commits to."""
+import math
+
+import pytest
+import torch
+
+import fused_attn
+from fused_attn import _hip, ops
+from helpers import TOL, announce, max_err, randn
+from oracle import attention_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    (1, 1, 1, 64, 64),
+    (2, 4, 4, 128, 128),
+    (1, 8, 2, 100, 100),  # GQA 4:1, ragged tails
+    (1, 4, 1, 37, 90),  # MQA, n_q < n_k (bottom-right causal)
+    (1, 2, 2, 90, 40),  # n_q > n_k: leading rows see no key
+    (3, 2, 2, 1, 257),  # single-token step below the split-K threshold
+    (2, 8, 2, 333, 333),
+    (1, 4, 1, 100, 500),
+    (1, 2, 2, 500, 100),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k", SHAPES)
+def test_prefill_matches_oracle(b, h_q, h_kv, n_q, n_k, causal, head_dim, dtype):
+    announce(f"prefill b={b} hq={h_q} hkv={h_kv} nq={n_q} nk={n_k} causal={causal} d={head_dim} {dtype}")
+    torch.manual_seed(0)
+    q = randn(b, h_q, n_q, head_dim, dtype=dtype)
+    k = randn(b, h_kv, n_k, head_dim, dtype=dtype)
+    v = randn(b, h_kv, n_k, head_dim, dtype=dtype)
+    assert ops._pick_backend(q, k) == "hip" and ops._hip_kernel_for(q, k) == "fwd"
+    out = fused_attn.attention(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal)
+    assert out.dtype == q.dtype and out.shape == q.shape
+    assert not torch.isnan(out).any()
+    assert max_err(out, ref) <= TOL[dtype]
+
+
+def test_custom_scale_and_negative_scale():
+    torch.manual_seed(0)
+    q, k, v = (randn(1, 2, 64, 64, dtype=torch.bfloat16) for _ in range(3))
+    for s in (0.05, -0.125):
+        announce(f"scale={s}")
+        out = fused_attn.attention(q, k, v, causal=True, scale=s)
+        ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=True, scale=s)
+        assert max_err(out, ref) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_noncontiguous_bnhd_layout(dtype):
+    """[B, N, H, D] storage (the usual HF layout) viewed as [B, H, N, D] (tests/test_correctness.py:97-106)."""
+    announce(f"bnhd view {dtype}")
+    torch.manual_seed(0)
+    x = randn(2, 64, 3, 4, 64, dtype=dtype)
+    q, k, v = (x[:, :, i].transpose(1, 2) for i in range(3))
+    assert not q.is_contiguous()
+    out = fused_attn.attention(q, k, v, causal=True)
+    ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=True)
+    assert out.stride() == q.stride() or out.is_contiguous()
+    assert max_err(out, ref) <= TOL[dtype]
+
+
+def test_unaligned_views_are_copied_not_misread():
+    announce("unaligned views")
+    torch.manual_seed(0)
+    base = randn(1, 2, 65 * 64 + 3, dtype=torch.bfloat16)
+    q = base[:, :, 3:].reshape(1, 2, 65, 64)[:, :, :64]  # data pointer 6 bytes past 16-byte alignment
+    k = randn(1, 2, 64, 64, dtype=torch.bfloat16)
+    v = randn(1, 2, 64, 64, dtype=torch.bfloat16)
+    out = fused_attn.attention(q, k, v)
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu())) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_lse_output(causal):
+    announce(f"lse causal={causal}")
+    torch.manual_seed(0)
+    q = randn(2, 8, 100, 128, dtype=torch.bfloat16)
+    k = randn(2, 2, 77, 128, dtype=torch.bfloat16)
+    v = randn(2, 2, 77, 128, dtype=torch.bfloat16)
+    out, lse = _hip.fwd(q, k, v, causal=causal, return_lse=True)
+    qf, kf = q.float().cpu(), orc.expand_kv(k.float().cpu(), 4)
+    s = torch.matmul(qf, kf.transpose(-1, -2)) / math.sqrt(128)
+    if causal:
+        s = s.masked_fill(~orc.causal_mask(100, 77), float("-inf"))
+    ref = torch.logsumexp(s, dim=-1)
+    got = lse.cpu()
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got))  # rows without keys report -inf
+    assert (got[fin] - ref[fin]).abs().max().item() < 1e-3
+
+
+def test_zero_sized_inputs():
+    announce("zero-sized")
+    q = torch.empty(0, 2, 16, 64, dtype=torch.bfloat16, device="cuda")
+    k = torch.empty(0, 2, 16, 64, dtype=torch.bfloat16, device="cuda")
+    assert fused_attn.attention(q, k, k).shape == q.shape
+    q = torch.empty(1, 2, 0, 64, dtype=torch.bfloat16, device="cuda")
+    assert fused_attn.attention(q, k[:1].expand(1, 2, 16, 64).contiguous(), k[:1].expand(1, 2, 16, 64).contiguous()).shape == q.shape
+    # n_k == 0: every row is empty -> zeros
+    q = randn(1, 2, 8, 64, dtype=torch.bfloat16)
+    kz = torch.empty(1, 2, 0, 64, dtype=torch.bfloat16, device="cuda")
+    assert torch.all(fused_attn.attention(q, kz, kz) == 0)
+
+
+def test_unsupported_dtype_raises_loudly():
+    q = randn(1, 2, 16, 64, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        _hip.fwd(q, q, q)
+
+
+# ---- BASELINE-sized workloads ------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(b=4, hq=32, hkv=8, n=4096, d=128, layout="bhnd"),
+    dict(b=4, hq=16, hkv=16, n=4096, d=64, layout="bhnd"),
+    dict(b=4, hq=32, hkv=8, n=4096, d=128, layout="bnhd"),
+])
+def test_baseline_prefill_configs(cfg):
+    """Causal bf16 prefill at the benchmark sizes; oracle in fp32 on the GPU, per (batch, kv group)."""
+    announce(f"baseline prefill {cfg}")
+    b, hq, hkv, n, d = cfg["b"], cfg["hq"], cfg["hkv"], cfg["n"], cfg["d"]
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    if cfg["layout"] == "bnhd":
+        q = randn(b, n, hq, d, dtype=torch.bfloat16, gen=gen).transpose(1, 2)
+        k = randn(b, n, hkv, d, dtype=torch.bfloat16, gen=gen).transpose(1, 2)
+        v = randn(b, n, hkv, d, dtype=torch.bfloat16, gen=gen).transpose(1, 2)
+    else:
+        q = randn(b, hq, n, d, dtype=torch.bfloat16, gen=gen)
+        k = randn(b, hkv, n, d, dtype=torch.bfloat16, gen=gen)
+        v = randn(b, hkv, n, d, dtype=torch.bfloat16, gen=gen)
+    out = fused_attn.attention(q, k, v, causal=True)
+    ref = orc.attention_chunked(q, k, v, causal=True)
+    err = max_err(out, ref)
+    print(f"max_abs_err={err:.3e}", flush=True)
+    assert err <= TOL[torch.bfloat16]

@@ -1,0 +1,90 @@
+"""Split-K flash-decoding on the HIP kernels vs the fp32 oracle
+(reference: tests/test_splitk_fp8.py:16-41), plus the BASELINE decode workloads."""
+import pytest
+import torch
+
+import fused_attn
+from fused_attn import _hip, ops
+from helpers import TOL, announce, max_err, randn
+from oracle import attention_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("num_splits", [1, 3, 8])
+@pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k,d",
+                         [(1, 2, 1, 1, 1000, 64), (2, 4, 2, 4, 777, 64), (1, 2, 2, 16, 2048, 128),
+                          (2, 32, 8, 1, 3000, 128), (1, 8, 1, 16, 2500, 128)])
+def test_splitk_matches_oracle(b, h_q, h_kv, n_q, n_k, d, num_splits, causal, dtype):
+    announce(f"splitk b={b} hq={h_q} hkv={h_kv} nq={n_q} nk={n_k} d={d} S={num_splits} causal={causal} {dtype}")
+    torch.manual_seed(0)
+    q = randn(b, h_q, n_q, d, dtype=dtype)
+    k = randn(b, h_kv, n_k, d, dtype=dtype)
+    v = randn(b, h_kv, n_k, d, dtype=dtype)
+    out = fused_attn.attention_splitk_triton(q, k, v, causal=causal, num_splits=num_splits)
+    ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal)
+    assert out.dtype == q.dtype and out.shape == q.shape
+    assert max_err(out, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("split_len", [64, 128, 192, 1024, 4096])
+def test_split_len_sweep(split_len):
+    announce(f"split_len={split_len}")
+    torch.manual_seed(1)
+    q = randn(2, 16, 2, 128, dtype=torch.bfloat16)
+    k = randn(2, 4, 2333, 128, dtype=torch.bfloat16)
+    v = randn(2, 4, 2333, 128, dtype=torch.bfloat16)
+    out = fused_attn.attention_splitk(q, k, v, causal=True, split_len=split_len)
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=True)) <= TOL[torch.bfloat16]
+
+
+def test_splitk_is_chosen_for_decode_shapes():
+    announce("dispatch decode")
+    torch.manual_seed(0)
+    q = randn(1, 8, 1, 64, dtype=torch.float16)
+    k = randn(1, 2, 4096, 64, dtype=torch.float16)
+    assert ops._pick_backend(q, k) == "hip" and ops._hip_kernel_for(q, k) == "splitk"
+    assert ops._hip_kernel_for(randn(1, 8, 512, 64, dtype=torch.float16), k) == "fwd"
+    out = fused_attn.attention(q, k, k, causal=True)
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), k.cpu(), causal=True)) <= TOL[torch.float16]
+
+
+def test_forced_splitk_backend_name(monkeypatch):
+    """FUSED_ATTN_BACKEND=splitk (a reference backend name) forces the split-K kernel for any shape."""
+    announce("forced splitk")
+    torch.manual_seed(0)
+    q = randn(1, 4, 70, 64, dtype=torch.bfloat16)
+    k = randn(1, 2, 300, 64, dtype=torch.bfloat16)
+    monkeypatch.setenv("FUSED_ATTN_BACKEND", "splitk")
+    assert ops._hip_kernel_for(q, k) == "splitk"
+    out = fused_attn.attention(q, k, k, causal=True)
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), k.cpu(), causal=True)) <= TOL[torch.bfloat16]
+
+
+def test_workspace_too_small_is_an_error():
+    q = randn(1, 4, 1, 64, dtype=torch.bfloat16)
+    k = randn(1, 2, 512, 64, dtype=torch.bfloat16)
+    ws = torch.empty(4, dtype=torch.float32, device="cuda")
+    need = _hip.workspace_bytes(1, 4, 1, 64, 4)
+    assert need == 1 * 4 * 1 * 4 * (64 + 2) * 4
+    out = _hip.splitk(q, k, k, split_len=128, workspace=ws)  # too small -> the wrapper allocates its own
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), k.cpu())) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("n_q,causal", [(1, False), (16, True)])
+def test_baseline_decode_configs(n_q, causal):
+    """B=32, Hq=32, Hkv=8, n_k=32768, D=128 bf16 with 128-key partitions (and the n_q=16 spec-decode shape)."""
+    announce(f"baseline decode nq={n_q} causal={causal}")
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q = randn(32, 32, n_q, 128, dtype=torch.bfloat16, gen=gen)
+    k = randn(32, 8, 32768, 128, dtype=torch.bfloat16, gen=gen)
+    v = randn(32, 8, 32768, 128, dtype=torch.bfloat16, gen=gen)
+    out = fused_attn.attention_splitk(q, k, v, causal=causal, split_len=128)
+    ref = orc.attention_chunked(q, k, v, causal=causal)
+    err = max_err(out, ref)
+    print(f"max_abs_err={err:.3e}", flush=True)
+    assert err <= TOL[torch.bfloat16]
+    # the public op picks split-K for this shape and gives the same bits
+    assert torch.equal(fused_attn.attention(q, k, v, causal=causal), out)

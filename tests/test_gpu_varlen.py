@@ -1,0 +1,85 @@
+"""Packed variable-length prefill on the HIP kernel vs the per-sequence fp32 oracle
+(reference: tests/test_varlen.py:15-43), plus the BASELINE varlen workload and a
+sentinel check that no row outside the sequences is written."""
+import pytest
+import torch
+
+import fused_attn
+from fused_attn import _hip
+from helpers import TOL, announce, max_err, randn
+from oracle import attention_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("lens", [[5, 33, 70], [1, 1, 1], [128], [64, 0, 17], [0], [0, 0, 3]])
+@pytest.mark.parametrize("h_q,h_kv", [(4, 4), (8, 2)])
+def test_varlen_matches_oracle(lens, causal, h_q, h_kv, dtype):
+    announce(f"varlen lens={lens} causal={causal} hq={h_q} hkv={h_kv} {dtype}")
+    torch.manual_seed(0)
+    d = 64
+    qs = [randn(n, h_q, d, dtype=dtype) for n in lens]
+    ks = [randn(n, h_kv, d, dtype=dtype) for n in lens]
+    vs = [randn(n, h_kv, d, dtype=dtype) for n in lens]
+    q, cu_q, max_q = fused_attn.pack_varlen(qs)
+    k, cu_k, max_k = fused_attn.pack_varlen(ks)
+    v, _, _ = fused_attn.pack_varlen(vs)
+    out = fused_attn.attention_varlen(q, k, v, cu_q, cu_k, max_q, max_k, causal=causal)
+    ref = orc.attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=causal)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    assert max_err(out, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_varlen_cross_attention_lengths(dtype):
+    """Different q and k lengths per sequence (chunked prefill against a KV cache)."""
+    announce(f"varlen cross {dtype}")
+    torch.manual_seed(0)
+    lq, lk = [8, 16, 0, 5], [40, 16, 7, 3]
+    q, cu_q, max_q = fused_attn.pack_varlen([randn(n, 4, 128, dtype=dtype) for n in lq])
+    k, cu_k, max_k = fused_attn.pack_varlen([randn(n, 2, 128, dtype=dtype) for n in lk])
+    v, _, _ = fused_attn.pack_varlen([randn(n, 2, 128, dtype=dtype) for n in lk])
+    for causal in (False, True):
+        out = fused_attn.attention_varlen(q, k, v, cu_q, cu_k, max_q, max_k, causal=causal)
+        ref = orc.attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=causal)
+        assert max_err(out, ref) <= TOL[dtype]
+
+
+def test_varlen_writes_only_sequence_rows():
+    """Rows past cu_seqlens_q[-1] (padding in a larger buffer) keep their sentinel bits."""
+    announce("varlen sentinel")
+    torch.manual_seed(0)
+    lens = [3, 0, 130, 1, 64]
+    total, pad = sum(lens), 37
+    q = randn(total + pad, 8, 128, dtype=torch.bfloat16)
+    k = randn(total + pad, 2, 128, dtype=torch.bfloat16)
+    v = randn(total + pad, 2, 128, dtype=torch.bfloat16)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+    sentinel = torch.full((total + pad, 8, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    out = _hip.varlen_fwd(q, k, v, cu, cu, max(lens), max(lens), causal=True, out=sentinel)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out[:total]).any()
+    assert torch.isnan(out[total:]).all()
+    ref = orc.attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), cu.cpu(), causal=True)
+    assert max_err(out[:total], ref[:total]) <= TOL[torch.bfloat16]
+
+
+def test_baseline_varlen_config():
+    """16 sequences, lengths ~U[0, 4096] by seed with one 0 and one 1; Hq=32, Hkv=8, D=128, bf16, causal."""
+    announce("baseline varlen")
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(0, 4097, (16,), generator=g).tolist()
+    lens[0], lens[1] = 0, 1
+    total = sum(lens)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    q = randn(total, 32, 128, dtype=torch.bfloat16, gen=gen)
+    k = randn(total, 8, 128, dtype=torch.bfloat16, gen=gen)
+    v = randn(total, 8, 128, dtype=torch.bfloat16, gen=gen)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+    out = fused_attn.attention_varlen(q, k, v, cu, cu, max(lens), max(lens), causal=True)
+    ref = orc.attention_varlen(q, k, v, cu, cu, causal=True)
+    err = max_err(out, ref)
+    print(f"lens={lens} max_abs_err={err:.3e}", flush=True)
+    assert err <= TOL[torch.bfloat16]

@@ -1,0 +1,183 @@
+"""Pins the oracle (oracle/attention_oracle.py) against library routines, an independent
+float64 brute force, closed forms and the reference's own known answers.  CPU only."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention_oracle as orc
+
+
+# ---- attention math ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", [1, 17, 128])
+def test_oracle_matches_sdpa(n, causal):
+    # reference: tests/test_correctness.py:32-39
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(2, 4, n, 64) for _ in range(3))
+    torch.testing.assert_close(orc.attention(q, k, v, causal=causal),
+                               F.scaled_dot_product_attention(q, k, v, is_causal=causal), atol=1e-5, rtol=1e-5)
+
+
+def test_oracle_gqa_equals_repeat_interleave_sdpa():
+    # reference: tests/test_correctness.py:42-50
+    torch.manual_seed(0)
+    q = torch.randn(1, 8, 32, 64)
+    k, v = torch.randn(1, 2, 32, 64), torch.randn(1, 2, 32, 64)
+    exp = F.scaled_dot_product_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), is_causal=True)
+    torch.testing.assert_close(orc.attention(q, k, v, causal=True), exp, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("n_q,n_k", [(37, 90), (90, 40), (1, 257), (5, 5)])
+def test_bottom_right_causal_matches_sdpa_with_explicit_mask(n_q, n_k):
+    torch.manual_seed(1)
+    q, k, v = torch.randn(1, 2, n_q, 32), torch.randn(1, 2, n_k, 32), torch.randn(1, 2, n_k, 32)
+    i = torch.arange(n_q)[:, None]
+    j = torch.arange(n_k)[None, :]
+    mask = j <= i + (n_k - n_q)
+    exp = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    exp = torch.where(mask.any(-1)[None, None, :, None], exp, torch.zeros_like(exp))  # empty rows -> 0
+    torch.testing.assert_close(orc.attention(q, k, v, causal=True), exp, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 4, 1, 37, 90, 16), (1, 2, 2, 9, 4, 8), (2, 4, 2, 13, 13, 32)])
+def test_oracle_matches_float64_bruteforce(shape, causal):
+    b, hq, hkv, nq, nk, d = shape
+    torch.manual_seed(2)
+    q, k, v = torch.randn(b, hq, nq, d), torch.randn(b, hkv, nk, d), torch.randn(b, hkv, nk, d)
+    ref = orc.attention_f64(q, k, v, causal=causal, scale=0.3)
+    np.testing.assert_allclose(orc.attention(q, k, v, causal=causal, scale=0.3).numpy(), ref, atol=2e-6, rtol=1e-5)
+
+
+def test_closed_forms():
+    torch.manual_seed(3)
+    v = torch.randn(1, 1, 6, 8)
+    k = torch.randn(1, 1, 6, 8)
+    q = torch.randn(1, 1, 6, 8)
+    out = orc.attention(q, k, v, causal=True)
+    torch.testing.assert_close(out[0, 0, 0], v[0, 0, 0])  # first causal row sees only key 0
+    # equal scores (zero queries) -> uniform weights -> running mean of the visible values
+    out0 = orc.attention(torch.zeros_like(q), k, v, causal=True)
+    means = torch.cumsum(v[0, 0], 0) / torch.arange(1, 7)[:, None]
+    torch.testing.assert_close(out0[0, 0], means)
+    # n_q > n_k: the first n_q - n_k rows see no key -> zeros
+    outz = orc.attention(torch.randn(1, 1, 5, 8), k[:, :, :2], v[:, :, :2], causal=True)
+    assert torch.all(outz[0, 0, :3] == 0) and torch.all(outz[0, 0, 3:].abs() > 0)
+
+
+def test_chunked_equals_whole():
+    torch.manual_seed(4)
+    q, k, v = torch.randn(2, 8, 70, 32), torch.randn(2, 2, 90, 32), torch.randn(2, 2, 90, 32)
+    for causal in (False, True):
+        whole = orc.attention(q, k, v, causal=causal)
+        for hpc, rpc in ((4, 0), (1, 16), (8, 7)):
+            torch.testing.assert_close(orc.attention_chunked(q, k, v, causal=causal, heads_per_chunk=hpc,
+                                                             rows_per_chunk=rpc), whole, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("lens_q,lens_k", [([5, 33, 70], [5, 33, 70]), ([64, 0, 17], [64, 0, 17]),
+                                           ([8, 16], [40, 16]), ([0, 1, 3], [2, 1, 0])])
+def test_varlen_oracle_matches_bruteforce(lens_q, lens_k):
+    torch.manual_seed(5)
+    hq, hkv, d = 4, 2, 16
+    q = torch.randn(sum(lens_q), hq, d)
+    k, v = torch.randn(sum(lens_k), hkv, d), torch.randn(sum(lens_k), hkv, d)
+    cq = torch.tensor([0] + list(np.cumsum(lens_q)), dtype=torch.int32)
+    ck = torch.tensor([0] + list(np.cumsum(lens_k)), dtype=torch.int32)
+    out = orc.attention_varlen(q, k, v, cq, ck, causal=True)
+    for i in range(len(lens_q)):
+        qs = q[cq[i]:cq[i + 1]].transpose(0, 1)[None]
+        if qs.shape[2] == 0:
+            continue
+        ks, vs = k[ck[i]:ck[i + 1]].transpose(0, 1)[None], v[ck[i]:ck[i + 1]].transpose(0, 1)[None]
+        ref = orc.attention_f64(qs, ks, vs, causal=True)[0].transpose(1, 0, 2)
+        np.testing.assert_allclose(out[cq[i]:cq[i + 1]].numpy(), ref, atol=2e-6, rtol=1e-5)
+    assert not torch.isnan(out).any()  # every packed row belongs to a sequence and is written
+
+
+# ---- FP8 ------------------------------------------------------------------------------------------
+
+
+@pytest.mark.skipif(orc.FP8_DTYPE is None, reason="torch build lacks float8")
+def test_e4m3fn_decode_table_matches_torch():
+    codes = torch.arange(256, dtype=torch.uint8)
+    got = codes.view(torch.float8_e4m3fn).float().tolist()
+    for c in range(256):
+        want = orc.e4m3fn_value(c)
+        if math.isnan(want):
+            assert math.isnan(got[c]), c
+        else:
+            assert got[c] == want, (c, got[c], want)
+
+
+@pytest.mark.skipif(orc.FP8_DTYPE is None, reason="torch build lacks float8")
+def test_fp8_roundtrip_bounds_and_scale_shape():
+    # reference: tests/test_splitk_fp8.py:53-62
+    torch.manual_seed(0)
+    k = torch.randn(2, 2, 200, 64) * 3
+    k8, ks = orc.quantize_kv_fp8(k)
+    assert k8.dtype == torch.float8_e4m3fn and ks.shape == (2, 2, 4)
+    kd = orc.dequantize_kv_fp8(k8, ks)
+    assert ((kd - k).abs() / k.abs().clamp_min(1e-3)).median() < 0.08
+    assert (kd - k).abs().max() / k.abs().max() < 0.07
+
+
+@pytest.mark.skipif(orc.FP8_DTYPE is None, reason="torch build lacks float8")
+def test_fp8_scales_equal_blockwise_amax():
+    torch.manual_seed(6)
+    x = torch.randn(1, 2, 130, 16)
+    _, s = orc.quantize_kv_fp8(x)
+    xn = x.numpy()
+    for h in range(2):
+        for blk in range(3):
+            amax = np.abs(xn[0, h, blk * 64:(blk + 1) * 64]).max()
+            assert s[0, h, blk].item() == pytest.approx(amax / 448.0, rel=1e-7)
+    # every quantised magnitude respects the E4M3 range and the block's scale
+    x8, s = orc.quantize_kv_fp8(x)
+    assert x8.float().abs().max() <= 448.0
+
+
+@pytest.mark.skipif(orc.FP8_DTYPE is None, reason="torch build lacks float8")
+def test_fp8_attention_accuracy_vs_fp32():
+    # reference: tests/test_splitk_fp8.py:65-74
+    torch.manual_seed(0)
+    q = torch.randn(2, 4, 8, 64)
+    k, v = torch.randn(2, 2, 300, 64), torch.randn(2, 2, 300, 64)
+    k8, ks = orc.quantize_kv_fp8(k)
+    v8, vs = orc.quantize_kv_fp8(v)
+    ref = orc.attention(q, k, v, causal=True)
+    out = orc.attention_fp8(q, k8, ks, v8, vs, causal=True)
+    assert (out - ref).abs().max() < 5e-2
+
+
+# ---- split-K --------------------------------------------------------------------------------------
+
+
+def test_choose_num_splits_known_answers():
+    # reference: tests/test_splitk_fp8.py:44-50
+    assert orc.choose_num_splits(1, 8, 32768, 1, num_sms=108) == 27
+    assert orc.choose_num_splits(64, 32, 32768, 1, num_sms=108) == 1
+    assert orc.choose_num_splits(1, 1, 512, 1, num_sms=108) == 2
+    assert orc.choose_num_splits(1, 1, 100000, 128, num_sms=108) == 1
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("split_len", [64, 128, 320, 4096])
+def test_splitk_combine_is_exact(causal, split_len):
+    torch.manual_seed(7)
+    q, k, v = torch.randn(1, 4, 4, 32), torch.randn(1, 2, 777, 32), torch.randn(1, 2, 777, 32)
+    o, m, l = orc.splitk_partials(q, k, v, causal, None, split_len)
+    comb = orc.splitk_combine(o, m, l)
+    np.testing.assert_allclose(comb, orc.attention_f64(q, k, v, causal=causal), atol=1e-12, rtol=1e-10)
+
+
+def test_split_len_alignment():
+    # reference: triton_splitk.py:153-154
+    assert orc.split_len_for(1000, 3) == 384 and -(-1000 // 384) == 3
+    assert orc.split_len_for(777, 8) == 128 and -(-777 // 128) == 7
+    assert orc.split_len_for(2048, 1) == 2048
