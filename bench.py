@@ -1,0 +1,219 @@
+"""Benchmark of the fused attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+
+One step = one call of ``fused_attn.attention`` on the causal GQA prefill
+workload B=4, Hq=32, Hkv=8, N=4096, D=128, bf16, [B,H,N,D], q/k/v ~ N(0,1)
+(the workload the headline metric is quoted on).  Inputs are resident in HBM
+before timing starts.  Printed as ONE JSON line:
+
+* ``value``: prefill TFLOP/s = 4*B*Hq*N^2*D/2 / (wall time per step)
+  (FLOP convention of benchmarks/bench.py:44-46 in the reference).
+* ``roofline``: the prefill kernel's algorithmic FLOPs / its average duration
+  from HIP events recorded around every launch on the launch stream, against
+  the 2516.6 TFLOP/s dense bf16 MFMA peak (256 CU x 4096 FLOP/clk x 2.4 GHz).
+  ``traffic`` is HBM bytes per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE
+  summary committed under profiles/ (null if absent).
+* ``decode``: split-K flash-decoding B=32, Hq=32, Hkv=8, n_q=1, n_k=32768,
+  D=128 bf16 with 128-key partitions; GB/s = (K+V+Q+O bytes) / time per call,
+  against 8 TB/s.  Also the n_q=16 causal spec-decode shape and the FP8 KV
+  cache (B=16, Hq=64, Hkv=8, n_k=65536).
+* ``cpu_baseline``: the unfused fp32 oracle on the host cores, timed on one
+  (batch, kv-head group) slice of the prefill workload (1/32 of it).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cuda-attention-kernels_amd"))
+
+MFMA_BF16_PEAK_TFLOPS = 2516.6
+HBM_PEAK_GBS = 8000.0
+PREFILL = dict(b=4, hq=32, hkv=8, n=4096, d=128)
+DECODE = dict(b=32, hq=32, hkv=8, nk=32768, d=128)
+FP8_DECODE = dict(b=16, hq=64, hkv=8, nk=65536, d=128)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "prefill_bf16_causal_b4_h32_n4096_d128_traffic.txt")
+
+
+def attn_flops(b, h, n, d, causal):
+    f = 4.0 * b * h * n * n * d
+    return f / 2 if causal else f
+
+
+def _time_calls(fn, steps, warmup):
+    """Wall time per call (synchronised both sides) and mean per-launch duration from HIP events."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    ev = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps / 1e3
+    return wall, ev
+
+
+def _traffic_bytes():
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    return float(m.group(1)) if m else None
+
+
+def bench_prefill(steps, warmup):
+    import torch
+
+    import fused_attn
+
+    c = PREFILL
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(c["b"], c["hq"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
+    k = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
+    v = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
+    out = fused_attn.attention(q, k, v, causal=True)
+    assert not torch.isnan(out).any()
+    wall, ev = _time_calls(lambda: fused_attn.attention(q, k, v, causal=True), steps, warmup)
+    flops = attn_flops(c["b"], c["hq"], c["n"], c["d"], True)
+    return flops, wall, ev
+
+
+def bench_decode(steps, warmup):
+    import torch
+
+    import fused_attn
+
+    res = {}
+    c = DECODE
+    g = torch.Generator(device="cuda").manual_seed(0)
+    k = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
+    v = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
+    for nq, causal in ((1, False), (16, True)):
+        q = torch.randn(c["b"], c["hq"], nq, c["d"], device="cuda", generator=g).bfloat16()
+        fn = lambda: fused_attn.attention_splitk(q, k, v, causal=causal, split_len=128)  # noqa: E731
+        wall, ev = _time_calls(fn, steps, warmup)
+        nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
+        key = "decode" if nq == 1 else "spec_decode_nq16"
+        res[key] = {
+            "workload": f"split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q={nq} n_k={c['nk']} D={c['d']} bf16"
+                        f"{' causal' if causal else ''}, 128-key partitions + LSE combine",
+            "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+            "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+        }
+    del k, v
+    torch.cuda.empty_cache()
+    c = FP8_DECODE
+    q = torch.randn(c["b"], c["hq"], 1, c["d"], device="cuda", generator=g).bfloat16()
+    k8, ks = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
+    v8, vs = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
+    torch.cuda.empty_cache()
+    fn = lambda: fused_attn.attention_fp8(q, k8, ks, v8, vs, split_len=128)  # noqa: E731
+    wall, ev = _time_calls(fn, steps, warmup)
+    nbytes = 2 * k8.numel() + 2 * ks.numel() * 4 + 2 * q.numel() * 2
+    res["fp8_decode"] = {
+        "workload": f"FP8-KV split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 n_k={c['nk']} D={c['d']}, "
+                    "e4m3fn + fp32 per-64-key scales, 128-key partitions",
+        "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+        "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    return res
+
+
+def cpu_baseline():
+    """The fp32 oracle on host cores over one (batch, kv-head group) slice of the prefill workload."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import attention_oracle as orc
+
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    c = PREFILL
+    g = c["hq"] // c["hkv"]
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(1, g, c["n"], c["d"], generator=gen).bfloat16()
+    k = torch.randn(1, 1, c["n"], c["d"], generator=gen).bfloat16()
+    v = torch.randn(1, 1, c["n"], c["d"], generator=gen).bfloat16()
+    for _ in range(2):
+        orc.attention(q, k, v, causal=True)
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        orc.attention(q, k, v, causal=True)
+    dt = (time.perf_counter() - t0) / reps
+    flops = attn_flops(1, g, c["n"], c["d"], True)
+    return {
+        "value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": f"unfused fp32 oracle, 1 of {c['b'] * c['hkv']} (batch, kv-head group) slices of the prefill "
+                  f"workload: 1x{g} q-heads x {c['n']}x{c['n']} causal, D={c['d']}; {dt * 1e3:.1f} ms per slice "
+                  f"(2 warm-up + {reps} timed)",
+        "ms_per_step_extrapolated": round(dt * c["b"] * c["hkv"] * 1e3, 1),
+    }
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-decode", action="store_true")
+    a = p.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the attention kernels run on a single MI355X "
+              "(multi-GPU sharding is a design note, not part of this build).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    flops, wall, ev = bench_prefill(a.steps, a.warmup)
+    achieved = flops / ev / 1e12
+    c = PREFILL
+    line = {
+        "metric": "prefill TFLOP/s bf16 causal N=4096 D=128; split-K decode achieved HBM GB/s",
+        "value": round(flops / wall / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: q/k/v ~ N(0,1) from a seeded generator, cast to bf16, resident in HBM",
+        "config": {"workload": f"causal GQA prefill B={c['b']} Hq={c['hq']} Hkv={c['hkv']} N={c['n']} D={c['d']} "
+                               "bf16 [B,H,N,D]", "batch": c["b"], "heads_q": c["hq"], "heads_kv": c["hkv"],
+                   "seq_len": c["n"], "head_dim": c["d"], "causal": True, "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": _traffic_bytes(), "kernel": "attn_tile_kernel<128,BF16,BF16,4,64,false>",
+                     "kernel_ms": round(ev * 1e3, 4)},
+    }
+    if not a.no_decode:
+        line["decode"] = bench_decode(max(5, a.steps), max(2, a.warmup))
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
