@@ -167,6 +167,27 @@ def cpu_baseline():
     }
 
 
+def copy_calibration(steps, warmup, nbytes=1 << 30):
+    """A plain device copy of known size: the yardstick for the PMC byte counters (FETCH_SIZE, WRITE_SIZE)."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    wall, ev = _time_calls(lambda: dst.copy_(src), steps, warmup)
+    return wall, ev, nbytes
+
+
+def run_only(which, steps, warmup):
+    if which == "prefill":
+        flops, wall, ev = bench_prefill(steps, warmup)
+        print(f"prefill: {flops / ev / 1e12:.1f} TFLOP/s kernel, {ev * 1e3:.4f} ms", flush=True)
+    elif which == "decode":
+        print(json.dumps(bench_decode(steps, warmup)), flush=True)
+    else:
+        wall, ev, nbytes = copy_calibration(steps, warmup)
+        print(f"copy {nbytes} B: {ev * 1e3:.4f} ms, {2 * nbytes / ev / 1e9:.1f} GB/s read+write", flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -174,6 +195,8 @@ def main():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+                   help="run one workload without the JSON line (for profiler runs)")
     a = p.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the attention kernels run on a single MI355X "
@@ -184,6 +207,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if a.only is not None:
+        run_only(a.only, a.steps, a.warmup)
+        return
     flops, wall, ev = bench_prefill(a.steps, a.warmup)
     achieved = flops / ev / 1e12
     c = PREFILL

@@ -103,6 +103,36 @@ __device__ __forceinline__ u32x2 fp8x4_to_e(uint32_t w) {
   return r;
 }
 
+// acc + lo + hi of a dword holding two 16-bit values, via v_dot2 with (1, 1):
+// the exact sum of the rounded values, one instruction per pair.
+template <class E>
+__device__ __forceinline__ float sum2(uint32_t w, float acc);
+template <>
+__device__ __forceinline__ float sum2<BF16>(uint32_t w, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+}
+template <>
+__device__ __forceinline__ float sum2<F16>(uint32_t w, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
+}
+
+// Raw buffer resource over [base, base + num_bytes): loads at offsets >= num_bytes
+// return zeros (hardware range check), which zero-fills tails without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, 0x00020000);
+}
+// 16-byte buffer load; STREAM sets the non-temporal hint for data read exactly once.
+template <bool STREAM>
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, STREAM ? 2 : 0);
+}
+
+// Online-softmax rescale threshold (log2 units): the running max is only
+// raised, and O rescaled, once a row's max grows by more than this.
+constexpr float kRescaleLog2 = 8.0f;
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float max_xor32(float x) {

@@ -90,9 +90,12 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   int seq_q = a.nq, seq_k = a.nk;
   int64_t qtok0 = 0, ktok0 = 0;
   if (!SPLIT && a.varlen) {
-    const int qs = a.cu_q[b], ks = a.cu_k[b];
-    seq_q = a.cu_q[b + 1] - qs;
-    seq_k = a.cu_k[b + 1] - ks;
+    // the offsets are the same for every lane: keep them (and all addresses derived
+    // from them) in scalar registers
+    const int qs = __builtin_amdgcn_readfirstlane(a.cu_q[b]);
+    const int ks = __builtin_amdgcn_readfirstlane(a.cu_k[b]);
+    seq_q = __builtin_amdgcn_readfirstlane(a.cu_q[b + 1]) - qs;
+    seq_k = __builtin_amdgcn_readfirstlane(a.cu_k[b + 1]) - ks;
     qtok0 = qs;
     ktok0 = ks;
   }
@@ -153,10 +156,14 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
     mask_from = min(khi, qlo + offset + 1);
   }
 
+  // K/V of this (batch, kv-head), read with buffer loads: a load past the
+  // resource's byte limit returns zeros, which zero-fills the keys >= khi of the
+  // last tile without branches (masked keys must not carry NaN/Inf into P*V).
   const uint8_t* kbase =
       (const uint8_t*)a.k + ((int64_t)b * a.skb + (int64_t)kvh * a.skh + ktok0 * a.skn) * KV::bytes;
   const uint8_t* vbase =
       (const uint8_t*)a.v + ((int64_t)b * a.svb + (int64_t)kvh * a.svh + ktok0 * a.svn) * KV::bytes;
+  const int64_t krow_bytes = a.skn * KV::bytes, vrow_bytes = a.svn * KV::bytes;
   const float* ksc = nullptr;
   const float* vsc = nullptr;
   if (KV::bytes == 1) {
@@ -164,32 +171,44 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
     vsc = a.v_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
   }
 
+  // A negative softmax scale is applied by negating Q (exact for 16-bit floats),
+  // so the kernel always works with c = |scale| * log2(e) >= 0 and max(c*s) = c*max(s).
+  const uint32_t qsign = a.qk_scale < 0.f ? 0x80008000u : 0u;
+  const float c_abs = fabsf(a.qk_scale);
+
   // ---- Q fragments (B operand of S^T), resident for the whole kernel -------------
   u32x4 qf[KS];
   {
     const uint16_t* qp =
         (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + (qtok0 + qi) * a.sqn + 8 * g;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = row_ok ? ld16(qp + 16 * s) : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s) qf[s] = row_ok ? (ld16(qp + 16 * s) ^ qsign) : u32x4{0, 0, 0, 0};
   }
 
   // ---- K/V staging: global -> VGPR -> LDS ----------------------------------------
   u32x4 kr[CPT], vr[CPT];
   auto gload = [&](int n0) {
+    // Byte limit = end of the tile's last key below khi.  It fits 32 bits (BN * row
+    // bytes < 2^31, checked at the C ABI) and is wave-uniform, so the descriptor lives
+    // in SGPRs.  Valid for any row stride, including 0 for a single-key cache.
+    const int valid = min(khi - n0, BN);
+    const uint32_t klim = __builtin_amdgcn_readfirstlane(
+        valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)krow_bytes + (uint32_t)(D * KV::bytes) : 0u);
+    const uint32_t vlim = __builtin_amdgcn_readfirstlane(
+        valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)vrow_bytes + (uint32_t)(D * KV::bytes) : 0u);
+    const auto rk = make_rsrc(kbase + (int64_t)n0 * krow_bytes, klim);
+    const auto rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, vlim);
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + i * NT;
       const int key = c / CPR, dc = c % CPR;
-      const int n = n0 + key;
-      if (n < khi) {
-        kr[i] = ld16(kbase + ((int64_t)n * a.skn + dc * EPC) * KV::bytes);
-        vr[i] = ld16(vbase + ((int64_t)n * a.svn + dc * EPC) * KV::bytes);
-      } else {  // zero-fill: masked keys must not carry NaN/Inf into P*V
-        kr[i] = u32x4{0, 0, 0, 0};
-        vr[i] = u32x4{0, 0, 0, 0};
-      }
+      kr[i] = buffer_load16<SPLIT>(rk, key * (int)krow_bytes + dc * 16);
+      vr[i] = buffer_load16<SPLIT>(rv, key * (int)vrow_bytes + dc * 16);
     }
   };
+  // K rows are stored at LDS row kperm(key) (bits 2 and 3 swapped), so the S^T
+  // A-operand reads consecutive LDS rows yet receives the key order whose C
+  // fragment hands each lane 8 contiguous keys per 16-key step.
   auto lstore = [&](int stage) {
     uint16_t* Ks = smem + stage * STAGE;
     uint16_t* Vs = Ks + KTILE;
@@ -197,14 +216,15 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + i * NT;
       const int key = c / CPR, dc = c % CPR;
+      const int krow_lds = (key & ~0xC) | ((key & 4) << 1) | ((key & 8) >> 1);
       if constexpr (KV::bytes == 2) {
-        st16(Ks + key * KLD + dc * 8, kr[i]);
+        st16(Ks + krow_lds * KLD + dc * 8, kr[i]);
         st16(Vs + key * VLD + dc * 8, vr[i]);
       } else {
         const u32x2 k0 = fp8x4_to_e<E>(kr[i][0]), k1 = fp8x4_to_e<E>(kr[i][1]);
         const u32x2 k2 = fp8x4_to_e<E>(kr[i][2]), k3 = fp8x4_to_e<E>(kr[i][3]);
-        st16(Ks + key * KLD + dc * 16, u32x4{k0[0], k0[1], k1[0], k1[1]});
-        st16(Ks + key * KLD + dc * 16 + 8, u32x4{k2[0], k2[1], k3[0], k3[1]});
+        st16(Ks + krow_lds * KLD + dc * 16, u32x4{k0[0], k0[1], k1[0], k1[1]});
+        st16(Ks + krow_lds * KLD + dc * 16 + 8, u32x4{k2[0], k2[1], k3[0], k3[1]});
         const u32x2 v0 = fp8x4_to_e<E>(vr[i][0]), v1 = fp8x4_to_e<E>(vr[i][1]);
         const u32x2 v2 = fp8x4_to_e<E>(vr[i][2]), v3 = fp8x4_to_e<E>(vr[i][3]);
         st16(Vs + key * VLD + dc * 16, u32x4{v0[0], v0[1], v1[0], v1[1]});
@@ -216,13 +236,13 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   f32x16 oacc[DB];
 #pragma unroll
   for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+  // Running max m_run (log2 domain, scaled) and this lane's share of the row sum.
   float m_run = NEG_INF, l_run = 0.f;
 
-  // A-operand row j of S^T reads key krow(j): swap the middle two quads of each 16.
-  const int krow = (j & 0x13) | ((j & 4) << 1) | ((j & 8) >> 1);
   // ds_read_b64_tr_b16 addressing for the V^T operand
   const int tr_i = lane & 15, tr_dh = (lane >> 4) & 1;
   const int tr_off = (8 * g + (tr_i >> 2)) * VLD + 16 * tr_dh + 4 * (tr_i & 3);
+  const int qlim = qi + offset;  // last key this lane's row may see (causal)
 
   if (n_tiles > 0) {
     gload(klo);
@@ -238,77 +258,108 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
       const uint16_t* Ks = smem + (t & 1) * STAGE;
       const uint16_t* Vs = Ks + KTILE;
 
-      // S^T = K Q^T
+      // S^T = K Q^T: all K fragments of a 32-key block are read before its MFMAs
       f32x16 sacc[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        sacc[kb] = f32x16{};
-        const uint16_t* kp = Ks + (kb * 32 + krow) * KLD + 8 * g;
+        u32x4 kf[KS];
+        const uint16_t* kp = Ks + (kb * 32 + j) * KLD + 8 * g;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) sacc[kb] = mfma32<E>(ld16(kp + 16 * s), qf[s], sacc[kb]);
+        for (int s = 0; s < KS; ++s) kf[s] = ld16(kp + 16 * s);
+        sacc[kb] = f32x16{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) sacc[kb] = mfma32<E>(kf[s], qf[s], sacc[kb]);
       }
 
-      // scale, mask, online softmax (log2 domain)
+      // per-block score scale (FP8: times the block's k_scale, fp8.py:104)
       float sc[KB], vs[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         if constexpr (KV::bytes == 1) {
           const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
-          sc[kb] = a.qk_scale * ksc[blk];
+          sc[kb] = c_abs * ksc[blk];
           vs[kb] = vsc[blk];
         } else {
-          sc[kb] = a.qk_scale;
+          sc[kb] = c_abs;
           vs[kb] = 1.f;
         }
       }
+
+      // tile max of the scaled scores (sc >= 0: max of sc*s is sc*max(s))
       const bool need_mask = n0 + BN > mask_from;
       float mt = NEG_INF;
+      if (!need_mask) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
+        for (int kb = 0; kb < KB; ++kb) {
+          float mx = sacc[kb][0];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = sacc[kb][r] * sc[kb];
-          if (need_mask) {
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+          mt = fmaxf(mt, mx * sc[kb]);
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          float mx = NEG_INF;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
             const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
-            const bool ok = n < khi && (!a.causal || n <= qi + offset);
-            x = ok ? x : NEG_INF;
+            const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
+            mx = fmaxf(mx, ok ? sacc[kb][r] : NEG_INF);
           }
-          sacc[kb][r] = x;
-          mt = fmaxf(mt, x);
+          mt = fmaxf(mt, mx == NEG_INF ? NEG_INF : mx * sc[kb]);
         }
       }
       mt = max_xor32(mt);
+
+      // Lazy rescale: keep the running max unless some row of the wave grew by
+      // more than 2^8; p = 2^(c*s - m_run) then stays <= 256 (no overflow risk),
+      // and O, l stay consistent because both use the same m_run.
       const float m_new = fmaxf(m_run, mt);
-      const float m_safe = (m_new == NEG_INF) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_safe);
+      if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
+        const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run - m_safe_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+        m_run = m_new;
+      }
+      const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
+
+      // P = 2^(c*s - m) as 16-bit B operands of PV
+      u32x4 pf[KB][2];
       float rs = 0.f;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
+        float p[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(sacc[kb][r] - m_safe);
-          sacc[kb][r] = p;
-          rs += p;
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(sacc[kb][r], sc[kb], -m_safe));
+        if (need_mask) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+            const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
+            p[r] = ok ? p[r] : 0.f;
+          }
         }
-      }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
-
-      // P^T as 16-bit B operands (v_scale folded in for FP8 K/V)
-      u32x4 pf[KB][2];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const float v = vs[kb];
-          pf[kb][h] = u32x4{pack2<E>(sacc[kb][8 * h + 0] * v, sacc[kb][8 * h + 1] * v),
-                            pack2<E>(sacc[kb][8 * h + 2] * v, sacc[kb][8 * h + 3] * v),
-                            pack2<E>(sacc[kb][8 * h + 4] * v, sacc[kb][8 * h + 5] * v),
-                            pack2<E>(sacc[kb][8 * h + 6] * v, sacc[kb][8 * h + 7] * v)};
+          if constexpr (KV::bytes == 1) {
+            // v_scale folded into P (the reference scales P.V by v_scale, fp8.py:116)
+            const float v = vs[kb];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
+            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0] * v, p[8 * h + 1] * v), pack2<E>(p[8 * h + 2] * v, p[8 * h + 3] * v),
+                              pack2<E>(p[8 * h + 4] * v, p[8 * h + 5] * v), pack2<E>(p[8 * h + 6] * v, p[8 * h + 7] * v)};
+          } else {
+            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0], p[8 * h + 1]), pack2<E>(p[8 * h + 2], p[8 * h + 3]),
+                              pack2<E>(p[8 * h + 4], p[8 * h + 5]), pack2<E>(p[8 * h + 6], p[8 * h + 7])};
+            // the row sum of the rounded P that the MFMA consumes (so O/l is a convex combination)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rs = sum2<E>(pf[kb][h][e], rs);
+          }
         }
       }
+      l_run += rs;
 
       // O^T += V^T P^T
 #pragma unroll

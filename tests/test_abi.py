@@ -86,6 +86,7 @@ def _params(**over):
     (dict(v=0), _hip.FA_ERR_INVALID_ARGUMENT, "non-NULL"),
     (dict(dtype=9), _hip.FA_ERR_INVALID_ARGUMENT, "unknown dtype"),
     (dict(scale=float("nan")), _hip.FA_ERR_INVALID_ARGUMENT, "NaN"),
+    (dict(k_stride_n=1 << 24), _hip.FA_ERR_UNSUPPORTED, "token stride"),
 ])
 def test_fwd_validation(lib, over, code, msg):
     p = _params(**over)

@@ -99,7 +99,9 @@ def test_lse_output(causal):
     got = lse.cpu()
     fin = torch.isfinite(ref)
     assert torch.equal(fin, torch.isfinite(got))  # rows without keys report -inf
-    assert (got[fin] - ref[fin]).abs().max().item() < 1e-3
+    # l sums the bf16-rounded P that the MFMA consumes, so the LSE carries bf16-level
+    # relative error in l: bound it by the bf16 resolution 2^-8
+    assert (got[fin] - ref[fin]).abs().max().item() < 2.0 ** -8
 
 
 def test_zero_sized_inputs():
