@@ -129,6 +129,22 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int off
   return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, STREAM ? 2 : 0);
 }
 
+// 16-byte buffer load written straight into LDS (no VGPRs): lane l's 16 bytes land at
+// lds + 16*l; `lds` must be wave-uniform.  Completion is tracked by vmcnt.
+template <bool STREAM>
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, int offset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, offset, 0, 0,
+                                           STREAM ? 2 : 0);
+#else
+  (void)r, (void)lds, (void)offset;
+#endif
+}
+// Wait until every outstanding vector-memory load of this wave (including LDS DMA) landed.
+__device__ __forceinline__ void lds_dma_wait() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained (gfx9 encoding)
+}
+
 // Online-softmax rescale threshold (log2 units): the running max is only
 // raised, and O rescaled, once a row's max grows by more than this.
 constexpr float kRescaleLog2 = 8.0f;

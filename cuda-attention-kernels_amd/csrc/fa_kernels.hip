@@ -32,39 +32,57 @@
 // stops issuing MFMAs past its own last visible key.
 #include <float.h>
 
-#include <mutex>
+#include <type_traits>
 
 #include "fa_device.hpp"
 #include "fa_internal.hpp"
 
 namespace fa {
 
-template <int D, int BN, int KVB>
+// LDS tile layout.  K and V tiles are [BN rows][D] 16-bit elements with no padding;
+// 16-byte chunks are XOR-swizzled per row so that every read pattern hits all 64
+// LDS banks once, and so that direct global->LDS loads (which write 64 lanes x 16 B
+// contiguously) can fill a tile.  Physical chunk = logical chunk ^ swizzle(row).
+template <int D, int BN>
 struct TileShape {
-  static constexpr int KLD = D + 8;   // K row stride in LDS (elements): 16 B pad, conflict-free b128 row reads
-  static constexpr int VLD = D + 16;  // V row stride: 32 B pad, conflict-free transposed reads
-  static constexpr int KTILE = BN * KLD;
-  static constexpr int VTILE = BN * VLD;
-  static constexpr int STAGE = KTILE + VTILE;
+  static constexpr int CPR = D / 8;             // 16-byte chunks per row
+  static constexpr int ROWS_PER_256B = 128 / D;  // rows sharing one 256-byte bank line
+  static constexpr int TILE = BN * D;            // elements per K (or V) tile
+  static constexpr int STAGE = 2 * TILE;         // K then V
   static constexpr size_t LDS_BYTES = 2 * STAGE * 2;
+  // K rows are read 16 at a time at one logical chunk: map them to 16 distinct bank groups.
+  __device__ static constexpr int swz_k(int row) { return (row / ROWS_PER_256B) % CPR; }
+  // V is read transposed: 4 consecutive rows (starting at a multiple of 4) x 4 chunks
+  // (starting at a multiple of 4) per 32 lanes.
+  __device__ static constexpr int swz_v(int row) {
+    return D == 128 ? 4 * (row & 3) + ((row >> 2) & 3) : 4 * ((row >> 1) & 1);
+  }
 };
 
 template <int D, class E, class KV, int NW, int BN, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) attn_tile_kernel(const TileArgs a) {
   constexpr int NT = NW * 64;
-  using Shape = TileShape<D, BN, KV::bytes>;
-  constexpr int KLD = Shape::KLD, VLD = Shape::VLD, KTILE = Shape::KTILE, STAGE = Shape::STAGE;
+  using Shape = TileShape<D, BN>;
+  constexpr int TILE = Shape::TILE, STAGE = Shape::STAGE, CPR = Shape::CPR;
   constexpr int KB = BN / 32;   // 32-key MFMA blocks per tile
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
   constexpr int DB = D / 32;    // 32-wide d blocks of O^T
-  constexpr int EPC = 16 / KV::bytes;  // K/V elements per 16-byte global chunk
-  constexpr int CPR = D / EPC;         // chunks per key row
-  constexpr int CPT = BN * CPR / NT;   // chunks per thread per tile
-  static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
-  static_assert((BN * CPR) % NT == 0, "tile must split evenly over the workgroup");
+  constexpr bool DIRECT = KV::bytes == 2;  // 16-bit K/V go global -> LDS without VGPRs
+  // direct loads: one wave instruction fills 1 KiB = 64 lanes x 16 B
+  constexpr int QPW = DIRECT ? (TILE * 2 / 1024) / NW : 1;
+  // staged FP8 loads: 16 e4m3 bytes per thread-chunk, widened to two 16-bit chunks
+  constexpr int CPR8 = D / 16;
+  constexpr int CPT8 = DIRECT ? 1 : BN * CPR8 / NT;
+  static_assert(BN % 32 == 0 && D % 32 == 0 && (D == 64 || D == 128), "tile shape");
+  static_assert(!DIRECT || (TILE * 2) % (1024 * NW) == 0, "direct loads must split evenly over the waves");
+  static_assert(DIRECT || (BN * CPR8) % NT == 0, "staged loads must split evenly over the workgroup");
   constexpr float NEG_INF = -__builtin_inff();
 
-  extern __shared__ __align__(16) uint16_t smem[];
+  // Two LDS stages as separate arrays: every access names its stage at compile time,
+  // so the compiler can tell that the DMA filling one stage never aliases reads of
+  // the other (and does not wait for the prefetch before reading the current tile).
+  __shared__ __align__(16) uint16_t lds_st0[STAGE];
+  __shared__ __align__(16) uint16_t lds_st1[STAGE];
 
   // ---- work item -------------------------------------------------------------------
   const int logical = xcd_remap((int)blockIdx.x, a.total);
@@ -123,7 +141,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 
   // ---- lane roles ------------------------------------------------------------------
   const int tid = (int)threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // wave index is uniform per wave: keep it (and every per-wave bound) in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int g = lane >> 5, j = lane & 31;
   const int wr0 = r0 + wave * 32;
   const int row = wr0 + j;
@@ -177,17 +196,23 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   const float c_abs = fabsf(a.qk_scale);
 
   // ---- Q fragments (B operand of S^T), resident for the whole kernel -------------
+  // (rows past the end read row 0 of the item, which exists, and are then zeroed:
+  // the loads stay unconditional and are all in flight together)
   u32x4 qf[KS];
   {
-    const uint16_t* qp =
-        (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + (qtok0 + qi) * a.sqn + 8 * g;
+    const int64_t qrow = qtok0 + (row_ok ? qi : 0);
+    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + qrow * a.sqn + 8 * g;
+    const uint32_t keep = row_ok ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = row_ok ? (ld16(qp + 16 * s) ^ qsign) : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s) qf[s] = (ld16(qp + 16 * s) ^ qsign) & keep;
   }
 
-  // ---- K/V staging: global -> VGPR -> LDS ----------------------------------------
-  u32x4 kr[CPT], vr[CPT];
-  auto gload = [&](int n0) {
+  // ---- K/V tiles: global -> LDS ---------------------------------------------------
+  // LDS row r of the K tile holds key kperm(r) (bits 2 and 3 swapped): the S^T
+  // A-operand then reads consecutive rows yet receives the key order whose C
+  // fragment hands each lane 8 contiguous keys per 16-key step.
+  auto kperm = [](int r) { return (r & ~0xC) | ((r & 4) << 1) | ((r & 8) >> 1); };
+  auto resources = [&](int n0, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv) {
     // Byte limit = end of the tile's last key below khi.  It fits 32 bits (BN * row
     // bytes < 2^31, checked at the C ABI) and is wave-uniform, so the descriptor lives
     // in SGPRs.  Valid for any row stride, including 0 for a single-key cache.
@@ -196,40 +221,55 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
         valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)krow_bytes + (uint32_t)(D * KV::bytes) : 0u);
     const uint32_t vlim = __builtin_amdgcn_readfirstlane(
         valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)vrow_bytes + (uint32_t)(D * KV::bytes) : 0u);
-    const auto rk = make_rsrc(kbase + (int64_t)n0 * krow_bytes, klim);
-    const auto rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, vlim);
+    rk = make_rsrc(kbase + (int64_t)n0 * krow_bytes, klim);
+    rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, vlim);
+  };
+  // 16-bit K/V: each wave fills QPW 1-KiB blocks of the stage straight from memory.
+  auto load_direct = [&](int n0, uint16_t* stage) {
+    __amdgpu_buffer_rsrc_t rk, rv;
+    resources(n0, rk, rv);
+    uint8_t* kl = (uint8_t*)stage;
+    uint8_t* vl = kl + TILE * 2;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
+    for (int i = 0; i < QPW; ++i) {
+      const int blk = wave * QPW + i;
+      const int byte = blk * 1024 + lane * 16;
+      const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
+      const int koff = kperm(r) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16);
+      const int voff = r * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16);
+      lds_dma16<SPLIT>(rk, kl + blk * 1024, koff);
+      lds_dma16<SPLIT>(rv, vl + blk * 1024, voff);
+    }
+  };
+  // FP8 K/V: staged through VGPRs and widened to E on the way into LDS.
+  u32x4 kr[CPT8], vr[CPT8];
+  auto load_staged = [&](int n0) {
+    __amdgpu_buffer_rsrc_t rk, rv;
+    resources(n0, rk, rv);
+#pragma unroll
+    for (int i = 0; i < CPT8; ++i) {
       const int c = tid + i * NT;
-      const int key = c / CPR, dc = c % CPR;
+      const int key = c / CPR8, dc = c % CPR8;
       kr[i] = buffer_load16<SPLIT>(rk, key * (int)krow_bytes + dc * 16);
       vr[i] = buffer_load16<SPLIT>(rv, key * (int)vrow_bytes + dc * 16);
     }
   };
-  // K rows are stored at LDS row kperm(key) (bits 2 and 3 swapped), so the S^T
-  // A-operand reads consecutive LDS rows yet receives the key order whose C
-  // fragment hands each lane 8 contiguous keys per 16-key step.
-  auto lstore = [&](int stage) {
-    uint16_t* Ks = smem + stage * STAGE;
-    uint16_t* Vs = Ks + KTILE;
+  auto store_staged = [&](uint16_t* stage) {
+    uint16_t* Ks = stage;
+    uint16_t* Vs = Ks + TILE;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
+    for (int i = 0; i < CPT8; ++i) {
       const int c = tid + i * NT;
-      const int key = c / CPR, dc = c % CPR;
-      const int krow_lds = (key & ~0xC) | ((key & 4) << 1) | ((key & 8) >> 1);
-      if constexpr (KV::bytes == 2) {
-        st16(Ks + krow_lds * KLD + dc * 8, kr[i]);
-        st16(Vs + key * VLD + dc * 8, vr[i]);
-      } else {
-        const u32x2 k0 = fp8x4_to_e<E>(kr[i][0]), k1 = fp8x4_to_e<E>(kr[i][1]);
-        const u32x2 k2 = fp8x4_to_e<E>(kr[i][2]), k3 = fp8x4_to_e<E>(kr[i][3]);
-        st16(Ks + krow_lds * KLD + dc * 16, u32x4{k0[0], k0[1], k1[0], k1[1]});
-        st16(Ks + krow_lds * KLD + dc * 16 + 8, u32x4{k2[0], k2[1], k3[0], k3[1]});
-        const u32x2 v0 = fp8x4_to_e<E>(vr[i][0]), v1 = fp8x4_to_e<E>(vr[i][1]);
-        const u32x2 v2 = fp8x4_to_e<E>(vr[i][2]), v3 = fp8x4_to_e<E>(vr[i][3]);
-        st16(Vs + key * VLD + dc * 16, u32x4{v0[0], v0[1], v1[0], v1[1]});
-        st16(Vs + key * VLD + dc * 16 + 8, u32x4{v2[0], v2[1], v3[0], v3[1]});
-      }
+      const int key = c / CPR8, dc = c % CPR8;
+      const int kr_row = kperm(key);
+      const u32x2 k0 = fp8x4_to_e<E>(kr[i][0]), k1 = fp8x4_to_e<E>(kr[i][1]);
+      const u32x2 k2 = fp8x4_to_e<E>(kr[i][2]), k3 = fp8x4_to_e<E>(kr[i][3]);
+      st16(Ks + kr_row * D + ((2 * dc) ^ Shape::swz_k(kr_row)) * 8, u32x4{k0[0], k0[1], k1[0], k1[1]});
+      st16(Ks + kr_row * D + ((2 * dc + 1) ^ Shape::swz_k(kr_row)) * 8, u32x4{k2[0], k2[1], k3[0], k3[1]});
+      const u32x2 v0 = fp8x4_to_e<E>(vr[i][0]), v1 = fp8x4_to_e<E>(vr[i][1]);
+      const u32x2 v2 = fp8x4_to_e<E>(vr[i][2]), v3 = fp8x4_to_e<E>(vr[i][3]);
+      st16(Vs + key * D + ((2 * dc) ^ Shape::swz_v(key)) * 8, u32x4{v0[0], v0[1], v1[0], v1[1]});
+      st16(Vs + key * D + ((2 * dc + 1) ^ Shape::swz_v(key)) * 8, u32x4{v2[0], v2[1], v3[0], v3[1]});
     }
   };
 
@@ -239,146 +279,190 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   // Running max m_run (log2 domain, scaled) and this lane's share of the row sum.
   float m_run = NEG_INF, l_run = 0.f;
 
-  // ds_read_b64_tr_b16 addressing for the V^T operand
+  // Per-lane LDS element offsets (within a stage) of the MFMA operand reads.
+  // K: S^T A-operand, row kb*32 + j, logical chunk 2s + g.
+  int koffs[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) koffs[s] = j * D + (((2 * s + g) ^ Shape::swz_k(j)) * 8);
+  // V: ds_read_b64_tr_b16 sources, rows 8g + 4*hi + (i >> 2) of each 16-key step,
+  // columns 32d + 16dh + 4(i & 3); the row term kb*32 + 16h is a constant offset.
   const int tr_i = lane & 15, tr_dh = (lane >> 4) & 1;
-  const int tr_off = (8 * g + (tr_i >> 2)) * VLD + 16 * tr_dh + 4 * (tr_i & 3);
+  int voffs[DB][2];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+      const int vr_row = 8 * g + 4 * hi + (tr_i >> 2);
+      const int col = 32 * d + 16 * tr_dh + 4 * (tr_i & 3);
+      voffs[d][hi] = vr_row * D + (((col >> 3) ^ Shape::swz_v(vr_row)) * 8) + (col & 7);
+    }
+  }
   const int qlim = qi + offset;  // last key this lane's row may see (causal)
 
   if (n_tiles > 0) {
-    gload(klo);
-    lstore(0);
+    if constexpr (DIRECT) {
+      load_direct(klo, lds_st0);
+    } else {
+      load_staged(klo);
+      store_staged(lds_st0);
+    }
   }
+  lds_dma_wait();
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
+  // One tile: prefetch tile t+1 into the other stage, then S^T, softmax, O += P V on
+  // this stage.  The stage is a compile-time choice (the loop below is unrolled by 2).
+  auto tile_step = [&](auto stage_tag, int t) {
+    constexpr int ST = decltype(stage_tag)::value;
+    uint16_t* cur = ST == 0 ? lds_st0 : lds_st1;
+    uint16_t* nxt = ST == 0 ? lds_st1 : lds_st0;
     const int n0 = klo + t * BN;
-    if (t + 1 < n_tiles) gload(n0 + BN);
-
-    if (wave_active && n0 < wave_khi) {
-      const uint16_t* Ks = smem + (t & 1) * STAGE;
-      const uint16_t* Vs = Ks + KTILE;
-
-      // S^T = K Q^T: all K fragments of a 32-key block are read before its MFMAs
-      f32x16 sacc[KB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        u32x4 kf[KS];
-        const uint16_t* kp = Ks + (kb * 32 + j) * KLD + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) kf[s] = ld16(kp + 16 * s);
-        sacc[kb] = f32x16{};
-#pragma unroll
-        for (int s = 0; s < KS; ++s) sacc[kb] = mfma32<E>(kf[s], qf[s], sacc[kb]);
-      }
-
-      // per-block score scale (FP8: times the block's k_scale, fp8.py:104)
-      float sc[KB], vs[KB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        if constexpr (KV::bytes == 1) {
-          const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
-          sc[kb] = c_abs * ksc[blk];
-          vs[kb] = vsc[blk];
-        } else {
-          sc[kb] = c_abs;
-          vs[kb] = 1.f;
-        }
-      }
-
-      // tile max of the scaled scores (sc >= 0: max of sc*s is sc*max(s))
-      const bool need_mask = n0 + BN > mask_from;
-      float mt = NEG_INF;
-      if (!need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          float mx = sacc[kb][0];
-#pragma unroll
-          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-          mt = fmaxf(mt, mx * sc[kb]);
-        }
+    if (t + 1 < n_tiles) {
+      if constexpr (DIRECT) {
+        load_direct(n0 + BN, nxt);  // released by the previous barrier
       } else {
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          float mx = NEG_INF;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
-            const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
-            mx = fmaxf(mx, ok ? sacc[kb][r] : NEG_INF);
-          }
-          mt = fmaxf(mt, mx == NEG_INF ? NEG_INF : mx * sc[kb]);
-        }
-      }
-      mt = max_xor32(mt);
-
-      // Lazy rescale: keep the running max unless some row of the wave grew by
-      // more than 2^8; p = 2^(c*s - m_run) then stays <= 256 (no overflow risk),
-      // and O, l stay consistent because both use the same m_run.
-      const float m_new = fmaxf(m_run, mt);
-      if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
-        const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run - m_safe_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
-        m_run = m_new;
-      }
-      const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
-
-      // P = 2^(c*s - m) as 16-bit B operands of PV
-      u32x4 pf[KB][2];
-      float rs = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        float p[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(sacc[kb][r], sc[kb], -m_safe));
-        if (need_mask) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
-            const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
-            p[r] = ok ? p[r] : 0.f;
-          }
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          if constexpr (KV::bytes == 1) {
-            // v_scale folded into P (the reference scales P.V by v_scale, fp8.py:116)
-            const float v = vs[kb];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
-            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0] * v, p[8 * h + 1] * v), pack2<E>(p[8 * h + 2] * v, p[8 * h + 3] * v),
-                              pack2<E>(p[8 * h + 4] * v, p[8 * h + 5] * v), pack2<E>(p[8 * h + 6] * v, p[8 * h + 7] * v)};
-          } else {
-            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0], p[8 * h + 1]), pack2<E>(p[8 * h + 2], p[8 * h + 3]),
-                              pack2<E>(p[8 * h + 4], p[8 * h + 5]), pack2<E>(p[8 * h + 6], p[8 * h + 7])};
-            // the row sum of the rounded P that the MFMA consumes (so O/l is a convex combination)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) rs = sum2<E>(pf[kb][h][e], rs);
-          }
-        }
-      }
-      l_run += rs;
-
-      // O^T += V^T P^T
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const uint16_t* vp = Vs + (kb * 32 + 16 * h) * VLD + d * 32 + tr_off;
-            const u32x2 lo = lds_read_tr16(vp);
-            const u32x2 hi = lds_read_tr16(vp + 4 * VLD);
-            oacc[d] = mfma32<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf[kb][h], oacc[d]);
-          }
-        }
+        load_staged(n0 + BN);
       }
     }
 
-    if (t + 1 < n_tiles) lstore((t + 1) & 1);
+      if (wave_active && n0 < wave_khi) {
+        const uint16_t* Ks = cur;
+        const uint16_t* Vs = cur + TILE;
+
+        // S^T = K Q^T.  The KB accumulation chains are independent; stepping them
+        // together keeps the MFMA pipe fed while each chain's last result is in flight.
+        f32x16 sacc[KB];
+  #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = f32x16{};
+        __builtin_amdgcn_s_setprio(1);
+  #pragma unroll
+        for (int s = 0; s < KS; ++s) {
+  #pragma unroll
+          for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32<E>(ld16(Ks + kb * 32 * D + koffs[s]), qf[s], sacc[kb]);
+        }
+        __builtin_amdgcn_s_setprio(0);
+
+        // per-block score scale (FP8: times the block's k_scale, fp8.py:104)
+        float sc[KB], vs[KB];
+  #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          if constexpr (KV::bytes == 1) {
+            const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
+            sc[kb] = c_abs * ksc[blk];
+            vs[kb] = vsc[blk];
+          } else {
+            sc[kb] = c_abs;
+            vs[kb] = 1.f;
+          }
+        }
+
+        // tile max of the scaled scores (sc >= 0: max of sc*s is sc*max(s))
+        const bool need_mask = n0 + BN > mask_from;
+        float mt = NEG_INF;
+        if (!need_mask) {
+  #pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            float mx = sacc[kb][0];
+  #pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+            mt = fmaxf(mt, mx * sc[kb]);
+          }
+        } else {
+  #pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            float mx = NEG_INF;
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+              const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
+              mx = fmaxf(mx, ok ? sacc[kb][r] : NEG_INF);
+            }
+            mt = fmaxf(mt, mx == NEG_INF ? NEG_INF : mx * sc[kb]);
+          }
+        }
+        mt = max_xor32(mt);
+
+        // Lazy rescale: keep the running max unless some row of the wave grew by
+        // more than 2^8; p = 2^(c*s - m_run) then stays <= 256 (no overflow risk),
+        // and O, l stay consistent because both use the same m_run.
+        const float m_new = fmaxf(m_run, mt);
+        if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
+          const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
+          const float alpha = fast_exp2(m_run - m_safe_new);
+          l_run *= alpha;
+  #pragma unroll
+          for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+          m_run = m_new;
+        }
+        const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
+
+        // P = 2^(c*s - m) as 16-bit B operands of PV
+        u32x4 pf[KB][2];
+        float rs = 0.f;
+  #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          float p[16];
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(sacc[kb][r], sc[kb], -m_safe));
+          if (need_mask) {
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+              const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
+              p[r] = ok ? p[r] : 0.f;
+            }
+          }
+  #pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            if constexpr (KV::bytes == 1) {
+              // v_scale folded into P (the reference scales P.V by v_scale, fp8.py:116)
+              const float v = vs[kb];
+  #pragma unroll
+              for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
+              pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0] * v, p[8 * h + 1] * v), pack2<E>(p[8 * h + 2] * v, p[8 * h + 3] * v),
+                                pack2<E>(p[8 * h + 4] * v, p[8 * h + 5] * v), pack2<E>(p[8 * h + 6] * v, p[8 * h + 7] * v)};
+            } else {
+              pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0], p[8 * h + 1]), pack2<E>(p[8 * h + 2], p[8 * h + 3]),
+                                pack2<E>(p[8 * h + 4], p[8 * h + 5]), pack2<E>(p[8 * h + 6], p[8 * h + 7])};
+              // the row sum of the rounded P that the MFMA consumes (so O/l is a convex combination)
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) rs = sum2<E>(pf[kb][h][e], rs);
+            }
+          }
+        }
+        l_run += rs;
+
+        // O^T += V^T P^T
+        __builtin_amdgcn_s_setprio(1);
+  #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+  #pragma unroll
+          for (int h = 0; h < 2; ++h) {
+  #pragma unroll
+            for (int d = 0; d < DB; ++d) {  // DB independent chains per 16-key step
+              const uint16_t* vp = Vs + (kb * 32 + 16 * h) * D;
+              const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
+              const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
+              oacc[d] = mfma32<E>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf[kb][h], oacc[d]);
+            }
+          }
+        }
+        __builtin_amdgcn_s_setprio(0);
+      }
+
+
+    if (t + 1 < n_tiles) {
+      if constexpr (DIRECT) {
+        lds_dma_wait();
+      } else {
+        store_staged(nxt);
+      }
+    }
     __syncthreads();
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   // ---- epilogue ----------------------------------------------------------------------
@@ -488,12 +572,8 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
 
 template <int D, class E, class KV, int NW, int BN, bool SPLIT>
 static hipError_t launch_tile(const TileArgs& a, hipStream_t stream) {
-  constexpr size_t lds = TileShape<D, BN, KV::bytes>::LDS_BYTES;
-  auto kern = attn_tile_kernel<D, E, KV, NW, BN, SPLIT>;
-  static const hipError_t attr_status =
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (attr_status != hipSuccess) return attr_status;
-  hipLaunchKernelGGL(kern, dim3((unsigned)a.total), dim3(NW * 64), lds, stream, a);
+  auto kern = attn_tile_kernel<D, E, KV, NW, BN, SPLIT>;  // LDS is static (two stages)
+  hipLaunchKernelGGL(kern, dim3((unsigned)a.total), dim3(NW * 64), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -583,7 +663,7 @@ static hipError_t launch_split_nw(const TileArgs& a, int nw, hipStream_t stream)
     case 1:
       return launch_tile<D, E, KV, 1, 32, true>(a, stream);
     case 2:
-      return launch_tile<D, E, KV, 2, 64, true>(a, stream);
+      return launch_tile<D, E, KV, 2, 32, true>(a, stream);
     default:
       return launch_tile<D, E, KV, 4, 64, true>(a, stream);
   }
