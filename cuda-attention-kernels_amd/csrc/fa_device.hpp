@@ -149,6 +149,9 @@ __device__ __forceinline__ void lds_dma_wait() {
 // raised, and O rescaled, once a row's max grows by more than this.
 constexpr float kRescaleLog2 = 8.0f;
 
+// Smallest score multiplier the kernels use (see the c_abs comment in the tile kernel).
+constexpr float kMinScale = 1e-30f;
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float max_xor32(float x) {

@@ -63,7 +63,7 @@ template <int D, class E, class KV, int NW, int BN, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) attn_tile_kernel(const TileArgs a) {
   constexpr int NT = NW * 64;
   using Shape = TileShape<D, BN>;
-  constexpr int TILE = Shape::TILE, STAGE = Shape::STAGE, CPR = Shape::CPR;
+  constexpr int TILE = Shape::TILE, STAGE = Shape::STAGE;
   constexpr int KB = BN / 32;   // 32-key MFMA blocks per tile
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
   constexpr int DB = D / 32;    // 32-wide d blocks of O^T
@@ -191,9 +191,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   }
 
   // A negative softmax scale is applied by negating Q (exact for 16-bit floats),
-  // so the kernel always works with c = |scale| * log2(e) >= 0 and max(c*s) = c*max(s).
+  // so the kernel always works with c = |scale| * log2(e) > 0 and max(c*s) = c*max(s).
+  // c is kept away from 0 so that a masked score (-inf) times c stays -inf; for a
+  // zero scale every 2^(c*s) is then 1 to float precision, as for c = 0.
   const uint32_t qsign = a.qk_scale < 0.f ? 0x80008000u : 0u;
-  const float c_abs = fabsf(a.qk_scale);
+  const float c_abs = fmaxf(fabsf(a.qk_scale), kMinScale);
 
   // ---- Q fragments (B operand of S^T), resident for the whole kernel -------------
   // (rows past the end read row 0 of the item, which exists, and are then zeroed:
@@ -348,7 +350,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
         for (int kb = 0; kb < KB; ++kb) {
           if constexpr (KV::bytes == 1) {
             const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
-            sc[kb] = c_abs * ksc[blk];
+            sc[kb] = fmaxf(c_abs * ksc[blk], kMinScale);
             vs[kb] = vsc[blk];
           } else {
             sc[kb] = c_abs;
@@ -356,29 +358,29 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
           }
         }
 
-        // tile max of the scaled scores (sc >= 0: max of sc*s is sc*max(s))
-        const bool need_mask = n0 + BN > mask_from;
-        float mt = NEG_INF;
-        if (!need_mask) {
+        // Masked tiles (the causal diagonal, the key tail) set excluded scores to -inf
+        // in one uniform block; exp2 then gives 0 for them, so the softmax below is the
+        // same straight-line code for every tile.
+        if (n0 + BN > mask_from) {
   #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
-            float mx = sacc[kb][0];
-  #pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-            mt = fmaxf(mt, mx * sc[kb]);
-          }
-        } else {
-  #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) {
-            float mx = NEG_INF;
   #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
               const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
-              mx = fmaxf(mx, ok ? sacc[kb][r] : NEG_INF);
+              sacc[kb][r] = ok ? sacc[kb][r] : NEG_INF;
             }
-            mt = fmaxf(mt, mx == NEG_INF ? NEG_INF : mx * sc[kb]);
           }
+        }
+
+        // tile max of the scaled scores (sc > 0: max of sc*s is sc*max(s))
+        float mt = NEG_INF;
+  #pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          float mx = sacc[kb][0];
+  #pragma unroll
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+          mt = fmaxf(mt, mx * sc[kb]);
         }
         mt = max_xor32(mt);
 
@@ -404,14 +406,6 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
           float p[16];
   #pragma unroll
           for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(sacc[kb][r], sc[kb], -m_safe));
-          if (need_mask) {
-  #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
-              const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
-              p[r] = ok ? p[r] : 0.f;
-            }
-          }
   #pragma unroll
           for (int h = 0; h < 2; ++h) {
             if constexpr (KV::bytes == 1) {
