@@ -48,6 +48,15 @@ struct CombineArgs {
 // workgroup shape chosen for a given row count G*Nq.
 int splitk_waves_for_rows(int rows);
 
+// TileArgs fields that prefill and split-K share (pointers, strides, heads, scale).
+TileArgs common_args(const fa_fwd_params& p);
+
+inline fa_status hip_status(hipError_t e, const char** err) {
+  if (e == hipSuccess) return FA_OK;
+  *err = hipGetErrorString(e);
+  return FA_ERR_HIP;
+}
+
 // Launchers.  They assume fa_abi.cpp has validated `p`.
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
 fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,

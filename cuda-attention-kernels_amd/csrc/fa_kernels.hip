@@ -36,28 +36,9 @@
 
 #include "fa_device.hpp"
 #include "fa_internal.hpp"
+#include "fa_tile.hpp"
 
 namespace fa {
-
-// LDS tile layout.  K and V tiles are [BN rows][D] 16-bit elements with no padding;
-// 16-byte chunks are XOR-swizzled per row so that every read pattern hits all 64
-// LDS banks once, and so that direct global->LDS loads (which write 64 lanes x 16 B
-// contiguously) can fill a tile.  Physical chunk = logical chunk ^ swizzle(row).
-template <int D, int BN>
-struct TileShape {
-  static constexpr int CPR = D / 8;             // 16-byte chunks per row
-  static constexpr int ROWS_PER_256B = 128 / D;  // rows sharing one 256-byte bank line
-  static constexpr int TILE = BN * D;            // elements per K (or V) tile
-  static constexpr int STAGE = 2 * TILE;         // K then V
-  static constexpr size_t LDS_BYTES = 2 * STAGE * 2;
-  // K rows are read 16 at a time at one logical chunk: map them to 16 distinct bank groups.
-  __device__ static constexpr int swz_k(int row) { return (row / ROWS_PER_256B) % CPR; }
-  // V is read transposed: 4 consecutive rows (starting at a multiple of 4) x 4 chunks
-  // (starting at a multiple of 4) per 32 lanes.
-  __device__ static constexpr int swz_v(int row) {
-    return D == 128 ? 4 * (row & 3) + ((row >> 2) & 3) : 4 * ((row >> 1) & 1);
-  }
-};
 
 template <int D, class E, class KV, int NW, int BN, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) attn_tile_kernel(const TileArgs a) {
@@ -209,11 +190,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
     for (int s = 0; s < KS; ++s) qf[s] = (ld16(qp + 16 * s) ^ qsign) & keep;
   }
 
-  // ---- K/V tiles: global -> LDS ---------------------------------------------------
-  // LDS row r of the K tile holds key kperm(r) (bits 2 and 3 swapped): the S^T
-  // A-operand then reads consecutive rows yet receives the key order whose C
-  // fragment hands each lane 8 contiguous keys per 16-key step.
-  auto kperm = [](int r) { return (r & ~0xC) | ((r & 4) << 1) | ((r & 8) >> 1); };
+  // ---- K/V tiles: global -> LDS (K rows permuted by kperm) ---------------------------
   auto resources = [&](int n0, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv) {
     // Byte limit = end of the tile's last key below khi.  It fits 32 bits (BN * row
     // bytes < 2^31, checked at the C ABI) and is wave-uniform, so the descriptor lives
@@ -577,13 +554,7 @@ static hipError_t launch_combine(const CombineArgs& c, int64_t rows, hipStream_t
   return hipGetLastError();
 }
 
-static fa_status hip_status(hipError_t e, const char** err) {
-  if (e == hipSuccess) return FA_OK;
-  *err = hipGetErrorString(e);
-  return FA_ERR_HIP;
-}
-
-static TileArgs common_args(const fa_fwd_params& p) {
+TileArgs common_args(const fa_fwd_params& p) {
   TileArgs a{};
   a.q = p.q;
   a.k = p.k;
@@ -609,44 +580,6 @@ static TileArgs common_args(const fa_fwd_params& p) {
   a.ssb = p.scale_stride_b;
   a.ssh = p.scale_stride_h;
   return a;
-}
-
-fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
-  constexpr int NW = 4, BN = 64;
-  TileArgs a = common_args(p);
-  a.o = p.o;
-  a.sob = p.o_stride_b;
-  a.soh = p.o_stride_h;
-  a.son = p.o_stride_n;
-  a.lse = p.lse;
-  a.slb = p.lse_stride_b;
-  a.slh = p.lse_stride_h;
-  a.varlen = varlen ? 1 : 0;
-  if (varlen) {
-    a.cu_q = p.cu_seqlens_q;
-    a.cu_k = p.cu_seqlens_k;
-    a.nq = p.max_seqlen_q;
-    a.nk = p.max_seqlen_k;
-    a.sqb = a.skb = a.svb = a.sob = 0;
-  }
-  if (a.nq <= 0 || p.batch <= 0) return FA_OK;
-  a.n_rowblk = (a.nq + NW * 32 - 1) / (NW * 32);
-  const int64_t total = (int64_t)p.batch * p.heads_q * a.n_rowblk;
-  if (total > INT32_MAX) {
-    *err = "grid too large";
-    return FA_ERR_UNSUPPORTED;
-  }
-  a.total = (int32_t)total;
-  a.n_split = 1;
-  a.split_len = 0;
-  hipError_t e = hipErrorInvalidValue;
-  const bool bf = p.dtype == FA_DTYPE_BF16;
-  if (p.head_dim == 128) {
-    e = bf ? launch_tile<128, BF16, BF16, NW, BN, false>(a, stream) : launch_tile<128, F16, F16, NW, BN, false>(a, stream);
-  } else if (p.head_dim == 64) {
-    e = bf ? launch_tile<64, BF16, BF16, NW, BN, false>(a, stream) : launch_tile<64, F16, F16, NW, BN, false>(a, stream);
-  }
-  return hip_status(e, err);
 }
 
 int splitk_waves_for_rows(int rows) { return rows <= 32 ? 1 : (rows <= 64 ? 2 : 4); }

@@ -1,0 +1,428 @@
+// Software-pipelined FlashAttention-2 prefill kernel for MI355X (gfx950).
+//
+// Serves the reference's dense and varlen prefill, attn_fwd_mma_kernel
+// (csrc/flash_attn_mma.cu:63-242) and _attn_fwd_kernel
+// (fused_attn/triton_fwd.py:85-172), for 16-bit Q/K/V with D in {64, 128}.
+//
+// A workgroup of 4 waves covers 128 queries of one q-head; wave w owns 32 of
+// them.  K and V stream through LDS in 64-key tiles, each in two buffers filled
+// straight from memory (buffer_load ... lds).  The product order per wave is the
+// same as in the split-K tile kernel (S^T = K Q^T with the softmax lane-local,
+// P^T kept in VGPRs as the B operand of O^T += V^T P^T), but the loop is
+// software-pipelined so that one wave always has matrix work and vector work
+// that do not depend on each other:
+//
+//   iteration t:  S_{t+1} = K_{t+1} Q^T            (MFMA)
+//                 P_t = 2^(c S_t - m), row sums    (VALU, exp)
+//                 O^T += V_t^T P_t^T               (MFMA)
+//                 max of S_{t+1}                   (VALU)
+//
+// MFMA and VALU instructions of one wave overlap when they are interleaved in
+// its own instruction stream; a wave that only issues MFMAs while another wave
+// of the SIMD only issues VALU work overlaps much less.  K therefore runs one
+// tile ahead of V: during iteration t the buffers hold K_{t+1} and V_t while
+// K_{t+2} and V_{t+1} are in flight into the other buffers.
+//
+// Element-wise masking is needed only on the causal diagonal and the key tail; it
+// sits behind a uniform branch after the main block, so an iteration is one basic
+// block apart from that and the rare online-softmax rescale.
+#include <float.h>
+
+#include <type_traits>
+
+#include "fa_device.hpp"
+#include "fa_internal.hpp"
+#include "fa_tile.hpp"
+
+namespace fa {
+
+template <int D, class E>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attn_fwd_kernel(const TileArgs a) {
+  constexpr int NW = 4, BN = 64;
+  using Shape = TileShape<D, BN>;
+  constexpr int TILE = Shape::TILE;
+  constexpr int KB = BN / 32;  // 32-key MFMA blocks per tile
+  constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
+  constexpr int DB = D / 32;   // 32-wide d blocks of O^T
+  constexpr int QPW = (TILE * 2 / 1024) / NW;  // 1-KiB DMA blocks per wave per K (or V) tile
+  static_assert(D == 64 || D == 128, "head dim");
+  static_assert((TILE * 2) % (1024 * NW) == 0, "direct loads must split evenly over the waves");
+  constexpr float NEG_INF = -__builtin_inff();
+
+  // Four separate arrays: every access names its buffer at compile time, so the
+  // compiler can tell that a DMA into one buffer never aliases reads of another.
+  __shared__ __align__(16) uint16_t k_buf0[TILE];
+  __shared__ __align__(16) uint16_t k_buf1[TILE];
+  __shared__ __align__(16) uint16_t v_buf0[TILE];
+  __shared__ __align__(16) uint16_t v_buf1[TILE];
+
+  // ---- work item: (batch, q-head, 128-query block) -----------------------------------
+  // xcd_remap hands each of the 8 XCDs a contiguous range of logical indices.  The
+  // (batch, q-head) pairs are cut into 8 groups, one per range, so that an XCD's L2
+  // sees the K/V of few kv-heads; within a group the query blocks are ordered by
+  // rank (heaviest causal blocks first), all heads of the group at each rank, which
+  // balances the XCD's CUs.
+  const int logical = xcd_remap((int)blockIdx.x, a.total);
+  const int nbh = a.total / a.n_rowblk;  // (batch, q-head) pairs
+  const int grp_heads = (nbh + 7) / 8;
+  const int grp = logical / (grp_heads * a.n_rowblk);
+  const int within = logical % (grp_heads * a.n_rowblk);
+  const int grp_size = min(grp_heads, nbh - grp * grp_heads);
+  const int mrev = within / grp_size;
+  int item = grp * grp_heads + within % grp_size;
+  const int gi = item % a.group;
+  item /= a.group;
+  const int kvh = item % a.hkv;
+  const int b = item / a.hkv;
+  const int hq = kvh * a.group + gi;
+  const int rb = a.causal ? (a.n_rowblk - 1 - mrev) : mrev;  // heaviest causal blocks first
+
+  int seq_q = a.nq, seq_k = a.nk;
+  int64_t qtok0 = 0, ktok0 = 0;
+  if (a.varlen) {
+    // the offsets are the same for every lane: keep them (and all addresses derived
+    // from them) in scalar registers
+    const int qs = __builtin_amdgcn_readfirstlane(a.cu_q[b]);
+    const int ks = __builtin_amdgcn_readfirstlane(a.cu_k[b]);
+    seq_q = __builtin_amdgcn_readfirstlane(a.cu_q[b + 1]) - qs;
+    seq_k = __builtin_amdgcn_readfirstlane(a.cu_k[b + 1]) - ks;
+    qtok0 = qs;
+    ktok0 = ks;
+  }
+  const int r0 = rb * NW * 32;
+  if (r0 >= seq_q) return;  // uniform over the workgroup (zero-length sequences exit here)
+  const int offset = seq_k - seq_q;  // bottom-right causal alignment (reference.py:24-33)
+
+  int khi = seq_k;
+  if (a.causal) khi = min(khi, min(r0 + NW * 32, seq_q) - 1 + offset + 1);
+  const int n_tiles = khi > 0 ? (khi + BN - 1) / BN : 0;
+  // Tiles [0, n_fast) hold only keys that every query of the workgroup sees.
+  const int wg_mask_from = a.causal ? min(khi, r0 + offset + 1) : khi;
+  const int n_fast = wg_mask_from > 0 ? wg_mask_from / BN : 0;
+
+  // ---- lane roles --------------------------------------------------------------------
+  const int tid = (int)threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int g = lane >> 5, j = lane & 31;
+  const int wr0 = r0 + wave * 32;
+  const int qi = wr0 + j;
+  const bool row_ok = qi < seq_q;
+  const bool wave_active = wr0 < seq_q;
+  // keys at or beyond mask_from are not visible to every row of this wave
+  int mask_from = khi;
+  if (a.causal && wave_active) mask_from = min(khi, wr0 + offset + 1);
+  const int qlim = qi + offset;  // last key this lane's row may see (causal)
+
+  const uint8_t* kbase = (const uint8_t*)a.k + ((int64_t)b * a.skb + (int64_t)kvh * a.skh + ktok0 * a.skn) * 2;
+  const uint8_t* vbase = (const uint8_t*)a.v + ((int64_t)b * a.svb + (int64_t)kvh * a.svh + ktok0 * a.svn) * 2;
+  const int64_t krow_bytes = a.skn * 2, vrow_bytes = a.svn * 2;
+
+  // A negative softmax scale is applied by negating Q (exact for 16-bit floats), so
+  // the kernel works with c = |scale| * log2(e) > 0 and max(c*s) = c*max(s).  c is
+  // kept away from 0 so that a masked score (-inf) times c stays -inf.
+  const uint32_t qsign = a.qk_scale < 0.f ? 0x80008000u : 0u;
+  const float c = fmaxf(fabsf(a.qk_scale), kMinScale);
+
+  // ---- Q fragments (B operand of S^T), resident for the whole kernel ----------------
+  // (rows past the end read row 0, which exists, and are zeroed)
+  u32x4 qf[KS];
+  {
+    const int64_t qrow = qtok0 + (row_ok ? qi : 0);
+    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + qrow * a.sqn + 8 * g;
+    const uint32_t keep = row_ok ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = (ld16(qp + 16 * s) ^ qsign) & keep;
+  }
+
+  // ---- K/V tiles: global -> LDS --------------------------------------------------------
+  // Buffer loads past the byte limit return zeros, which zero-fills the keys >= khi of
+  // the last tile (masked keys must not carry NaN/Inf into P*V).  The limit fits 32 bits
+  // (row stride checked at the C ABI) and is wave-uniform, so descriptors live in SGPRs.
+  auto limit = [&](int n0, int64_t row_bytes) {
+    const int valid = min(khi - n0, BN);
+    return __builtin_amdgcn_readfirstlane(valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)row_bytes + (uint32_t)(D * 2)
+                                                    : 0u);
+  };
+  auto load_k = [&](int n0, uint16_t* dst) {
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)n0 * krow_bytes, limit(n0, krow_bytes));
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+      const int blk = wave * QPW + i;
+      const int byte = blk * 1024 + lane * 16;
+      const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
+      lds_dma16<false>(rk, (uint8_t*)dst + blk * 1024, kperm(r) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16));
+    }
+  };
+  auto load_v = [&](int n0, uint16_t* dst) {
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, limit(n0, vrow_bytes));
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+      const int blk = wave * QPW + i;
+      const int byte = blk * 1024 + lane * 16;
+      const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
+      lds_dma16<false>(rv, (uint8_t*)dst + blk * 1024, r * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16));
+    }
+  };
+
+  // Per-lane LDS element offsets of the MFMA operand reads.
+  // K: S^T A-operand, row kb*32 + j, logical chunk 2s + g.
+  int koffs[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) koffs[s] = j * D + (((2 * s + g) ^ Shape::swz_k(j)) * 8);
+  // V: ds_read_b64_tr_b16 sources, rows 8g + 4*hi + (i >> 2) of each 16-key step,
+  // columns 32d + 16dh + 4(i & 3); the row term kb*32 + 16h is a constant offset.
+  const int tr_i = lane & 15, tr_dh = (lane >> 4) & 1;
+  int voffs[DB][2];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+      const int vr_row = 8 * g + 4 * hi + (tr_i >> 2);
+      const int col = 32 * d + 16 * tr_dh + 4 * (tr_i & 3);
+      voffs[d][hi] = vr_row * D + (((col >> 3) ^ Shape::swz_v(vr_row)) * 8) + (col & 7);
+    }
+  }
+
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+  // running max m_run (log2 domain, scaled) and this lane's share of the row sum
+  float m_run = NEG_INF, l_run = 0.f;
+  // S^T of two consecutive tiles (the loop below is unrolled by 2)
+  f32x16 s_a[KB], s_b[KB];
+
+  // ---- building blocks ---------------------------------------------------------------
+  auto qk = [&](const uint16_t* Ks, f32x16(&acc)[KB], int s) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma32<E>(ld16(Ks + kb * 32 * D + koffs[s]), qf[s], acc[kb]);
+  };
+  // excluded scores of tile t (keys n0..n0+BN) -> -inf
+  auto mask = [&](f32x16(&sc)[KB], int n0) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+        const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
+        sc[kb][r] = ok ? sc[kb][r] : NEG_INF;
+      }
+    }
+  };
+  // row max of c*S over the tile (both lanes of the row agree)
+  auto tile_max = [&](const f32x16(&sc)[KB]) {
+    float mx = sc[0][0];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int r = (kb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
+    }
+    return max_xor32(mx * c);
+  };
+  // Lazy rescale: keep the running max unless some row of the wave grew by more
+  // than 2^8; p = 2^(c*s - m_run) then stays <= 256, and O, l stay consistent
+  // because both use the same m_run.
+  auto update_max = [&](float mt) {
+    const float m_new = fmaxf(m_run, mt);
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
+      const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - m_safe_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+      m_run = m_new;
+    }
+  };
+  // One pipelined iteration on tile t: S_{t+1} from K buffer Kn, P_t from cur,
+  // O += V_t P_t from V buffer Vc, then the row max of S_{t+1}.  The max is taken
+  // unmasked inside the main block and recomputed only when tile t+1 is masked
+  // (or does not exist), so the common path is one basic block.
+  auto body = [&](const uint16_t* Kn, const uint16_t* Vc, f32x16(&cur)[KB], f32x16(&nxt)[KB], int t)
+      __attribute__((always_inline)) {
+    // MFMA slots m = 0 .. NQK-1: S_{t+1} (k-step m / KB, key block m % KB);
+    // m = NQK .. NM-1: O += V_t P_t (key block, 16-key half, d block; d fastest).
+    // The LDS operand of slot m is read PD slots ahead into a ring of registers,
+    // so its latency (about two MFMAs) is hidden behind the MFMAs in between; a
+    // sched_barrier after every slot keeps this order through scheduling.
+    constexpr int NQK = KS * KB, NPV = KB * 2 * DB, NM = NQK + NPV, PD = 3;
+    constexpr int NEXP = KB * 8;         // exp micro-steps (2 scores each) for S_t
+    constexpr int EPS = NEXP / NQK;      // micro-steps per S MFMA slot
+    constexpr int NMAX = KB * 8;         // max3 steps for S_{t+1}
+    static_assert(NEXP % NQK == 0, "exp steps must spread evenly over the S slots");
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) nxt[kb] = f32x16{};
+    const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
+    u32x4 pf[KB][2];
+    u32x4 opnd[PD + 1];
+    float rs = 0.f;
+    float mx = NEG_INF;
+
+    auto read = [&](int m) __attribute__((always_inline)) {
+      if (m < NQK) {
+        const int s = m / KB, kb = m % KB;
+        opnd[m % (PD + 1)] = ld16(Kn + kb * 32 * D + koffs[s]);
+      } else {
+        const int i = m - NQK, kb = i / (2 * DB), h = (i / DB) % 2, d = i % DB;
+        const uint16_t* vp = Vc + (kb * 32 + 16 * h) * D;
+        const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
+        const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
+        opnd[m % (PD + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+    };
+    // exp micro-step u: scores 2e and 2e+1 of chunk (kb, h) of S_t
+    auto exp_step = [&](int u) __attribute__((always_inline)) {
+      const int kb = u / 8, h = (u / 4) % 2, e = u % 4;
+      const float p0 = fast_exp2(__builtin_fmaf(cur[kb][8 * h + 2 * e], c, -m_safe));
+      const float p1 = fast_exp2(__builtin_fmaf(cur[kb][8 * h + 2 * e + 1], c, -m_safe));
+      const uint32_t pk = pack2<E>(p0, p1);
+      pf[kb][h][e] = pk;
+      // the row sum of the rounded P that the MFMA consumes (so O/l is a convex combination)
+      rs = sum2<E>(pk, rs);
+    };
+    // max step v: scores 2v and 2v+1 of S_{t+1}
+    auto max_step = [&](int v) __attribute__((always_inline)) {
+      const int kb = v / 8, r = 2 * (v % 8);
+      mx = fmaxf(mx, fmaxf(nxt[kb][r], nxt[kb][r + 1]));
+    };
+
+#pragma unroll
+    for (int m = 0; m < PD; ++m) read(m);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      if (m + PD < NM) read(m + PD);
+      const u32x4 op = opnd[m % (PD + 1)];
+      if (m < NQK) {
+        const int s = m / KB, kb = m % KB;
+        nxt[kb] = mfma32<E>(op, qf[s], nxt[kb]);
+#pragma unroll
+        for (int q = 0; q < EPS; ++q) exp_step(m * EPS + q);
+      } else {
+        const int i = m - NQK, kb = i / (2 * DB), h = (i / DB) % 2, d = i % DB;
+        oacc[d] = mfma32<E>(op, pf[kb][h], oacc[d]);
+        // S_{t+1} is complete two slots after its last MFMA was issued
+        const int v0 = (i - 2) * NMAX / (NPV - 2), v1 = (i - 1) * NMAX / (NPV - 2);
+        if (i >= 2) {
+#pragma unroll
+          for (int v = v0; v < v1; ++v) max_step(v);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l_run += rs;
+    float mt = max_xor32(mx * c);
+    if (t + 1 >= n_fast) {
+      const int n1 = (t + 1) * BN;
+      if (t + 1 < n_tiles) {
+        if (n1 + BN > mask_from) {
+          mask(nxt, n1);
+          mt = tile_max(nxt);
+        }
+      } else {
+        mt = NEG_INF;  // past the last tile: nxt holds stale LDS data and is discarded
+      }
+    }
+    update_max(mt);
+  };
+
+  // ---- prologue: K_0, V_0, K_1 in flight; S_0 and its max ------------------------------
+  if (n_tiles > 0) {
+    load_k(0, k_buf0);
+    load_v(0, v_buf0);
+    if (n_tiles > 1) load_k(BN, k_buf1);
+    lds_dma_wait();
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) s_a[kb] = f32x16{};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qk(k_buf0, s_a, s);
+    if (BN > mask_from) mask(s_a, 0);
+    update_max(tile_max(s_a));
+    __syncthreads();  // every wave has read K_0: its buffer takes K_2
+  }
+
+  // ---- main loop, unrolled by 2 so that every buffer is named at compile time --------
+  auto step = [&](auto stage_tag, int t) __attribute__((always_inline)) {
+    constexpr int ST = decltype(stage_tag)::value;
+    uint16_t* k_this = ST == 0 ? k_buf0 : k_buf1;  // held K_t (read already), takes K_{t+2}
+    uint16_t* k_next = ST == 0 ? k_buf1 : k_buf0;  // holds K_{t+1}
+    uint16_t* v_this = ST == 0 ? v_buf0 : v_buf1;  // holds V_t
+    uint16_t* v_next = ST == 0 ? v_buf1 : v_buf0;  // takes V_{t+1}
+    if (t + 2 < n_tiles) load_k((t + 2) * BN, k_this);
+    if (t + 1 < n_tiles) load_v((t + 1) * BN, v_next);
+    auto& cur = ST == 0 ? s_a : s_b;
+    auto& nxt = ST == 0 ? s_b : s_a;
+    body(k_next, v_this, cur, nxt, t);
+    lds_dma_wait();
+    __syncthreads();
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < n_tiles) step(std::integral_constant<int, 1>{}, t + 1);
+  }
+
+  // ---- epilogue ------------------------------------------------------------------------
+  if (!wave_active) return;
+  const float l_tot = sum_xor32(l_run);  // each lane summed its 16 of the row's keys per tile
+  if (!row_ok) return;
+  // Rows that saw no key have l == 0 and emit zeros (triton_fwd.py:163-165).
+  const float l_safe = (l_tot == 0.f) ? 1.f : l_tot;
+  const float inv = 1.f / l_safe;
+  uint16_t* op = (uint16_t*)a.o + (int64_t)b * a.sob + (int64_t)hq * a.soh + (qtok0 + qi) * a.son;
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d0 = d * 32 + 8 * rq + 4 * g;
+      st8(op + d0, u32x2{pack2<E>(oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv),
+                         pack2<E>(oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv)});
+    }
+  }
+  if (a.lse != nullptr && g == 0) {
+    // natural-log LSE (triton_fwd.py:169-172)
+    a.lse[(int64_t)b * a.slb + (int64_t)hq * a.slh + qi] = (m_run + __log2f(l_safe)) * kLn2;
+  }
+}
+
+template <int D, class E>
+static hipError_t launch_fwd(const TileArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3((unsigned)a.total), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
+  TileArgs a = common_args(p);
+  a.o = p.o;
+  a.sob = p.o_stride_b;
+  a.soh = p.o_stride_h;
+  a.son = p.o_stride_n;
+  a.lse = p.lse;
+  a.slb = p.lse_stride_b;
+  a.slh = p.lse_stride_h;
+  a.varlen = varlen ? 1 : 0;
+  if (varlen) {
+    a.cu_q = p.cu_seqlens_q;
+    a.cu_k = p.cu_seqlens_k;
+    a.nq = p.max_seqlen_q;
+    a.nk = p.max_seqlen_k;
+    a.sqb = a.skb = a.svb = a.sob = 0;
+  }
+  if (a.nq <= 0 || p.batch <= 0) return FA_OK;
+  a.n_rowblk = (a.nq + 127) / 128;
+  const int64_t total = (int64_t)p.batch * p.heads_q * a.n_rowblk;
+  if (total > INT32_MAX) {
+    *err = "grid too large";
+    return FA_ERR_UNSUPPORTED;
+  }
+  a.total = (int32_t)total;
+  a.n_split = 1;
+  a.split_len = 0;
+  hipError_t e = hipErrorInvalidValue;
+  const bool bf = p.dtype == FA_DTYPE_BF16;
+  if (p.head_dim == 128) {
+    e = bf ? launch_fwd<128, BF16>(a, stream) : launch_fwd<128, F16>(a, stream);
+  } else if (p.head_dim == 64) {
+    e = bf ? launch_fwd<64, BF16>(a, stream) : launch_fwd<64, F16>(a, stream);
+  }
+  return hip_status(e, err);
+}
+
+}  // namespace fa

@@ -1,0 +1,32 @@
+// LDS tile layout shared by the prefill and split-K kernels.
+#pragma once
+
+#include "fa_device.hpp"
+
+namespace fa {
+
+// K and V tiles are [BN rows][D] 16-bit elements with no padding; 16-byte chunks
+// are XOR-swizzled per row so that every read pattern hits all 64 LDS banks once,
+// and so that direct global->LDS loads (which write 64 lanes x 16 B contiguously)
+// can fill a tile.  Physical chunk = logical chunk ^ swizzle(row).
+template <int D, int BN>
+struct TileShape {
+  static constexpr int CPR = D / 8;             // 16-byte chunks per row
+  static constexpr int ROWS_PER_256B = 128 / D;  // rows sharing one 256-byte bank line
+  static constexpr int TILE = BN * D;            // elements per K (or V) tile
+  static constexpr int STAGE = 2 * TILE;         // K then V
+  // K rows are read 16 at a time at one logical chunk: map them to 16 distinct bank groups.
+  __device__ static constexpr int swz_k(int row) { return (row / ROWS_PER_256B) % CPR; }
+  // V is read transposed: 4 consecutive rows (starting at a multiple of 4) x 4 chunks
+  // (starting at a multiple of 4) per 32 lanes.
+  __device__ static constexpr int swz_v(int row) {
+    return D == 128 ? 4 * (row & 3) + ((row >> 2) & 3) : 4 * ((row >> 1) & 1);
+  }
+};
+
+// LDS row r of a K tile holds key kperm(r) (bits 2 and 3 swapped): the S^T
+// A-operand then reads consecutive rows yet receives the key order whose C
+// fragment hands each lane 8 contiguous keys per 16-key step.
+__device__ __forceinline__ constexpr int kperm(int r) { return (r & ~0xC) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+}  // namespace fa
