@@ -103,15 +103,17 @@ def bench_decode(steps, warmup):
     g = torch.Generator(device="cuda").manual_seed(0)
     k = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
     v = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
-    for nq, causal in ((1, False), (16, True)):
+    for nq, causal, split in ((1, False, 128), (16, True, 128), (1, False, None), (16, True, None)):
         q = torch.randn(c["b"], c["hq"], nq, c["d"], device="cuda", generator=g).bfloat16()
-        fn = lambda: fused_attn.attention_splitk(q, k, v, causal=causal, split_len=128)  # noqa: E731
+        fn = lambda: fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split)  # noqa: E731
         wall, ev = _time_calls(fn, steps, warmup)
         nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
-        key = "decode" if nq == 1 else "spec_decode_nq16"
+        key = ("decode" if nq == 1 else "spec_decode_nq16") + ("" if split else "_default_split")
+        keys = split or fused_attn.ops.default_split_len(nq, c["nk"], c["b"], c["hkv"], c["hq"] // c["hkv"])
         res[key] = {
             "workload": f"split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q={nq} n_k={c['nk']} D={c['d']} bf16"
-                        f"{' causal' if causal else ''}, 128-key partitions + LSE combine",
+                        f"{' causal' if causal else ''}, {keys}-key partitions + LSE combine"
+                        f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
             "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
@@ -123,16 +125,19 @@ def bench_decode(steps, warmup):
     k8, ks = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
     v8, vs = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
     torch.cuda.empty_cache()
-    fn = lambda: fused_attn.attention_fp8(q, k8, ks, v8, vs, split_len=128)  # noqa: E731
-    wall, ev = _time_calls(fn, steps, warmup)
-    nbytes = 2 * k8.numel() + 2 * ks.numel() * 4 + 2 * q.numel() * 2
-    res["fp8_decode"] = {
-        "workload": f"FP8-KV split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 n_k={c['nk']} D={c['d']}, "
-                    "e4m3fn + fp32 per-64-key scales, 128-key partitions",
-        "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
-        "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
-    }
+    for split in (128, None):
+        fn = lambda: fused_attn.attention_fp8(q, k8, ks, v8, vs, split_len=split)  # noqa: E731
+        wall, ev = _time_calls(fn, steps, warmup)
+        nbytes = 2 * k8.numel() + 2 * ks.numel() * 4 + 2 * q.numel() * 2
+        keys = split or fused_attn.ops.default_split_len(1, c["nk"], c["b"], c["hkv"], c["hq"] // c["hkv"])
+        res["fp8_decode" + ("" if split else "_default_split")] = {
+            "workload": f"FP8-KV split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 n_k={c['nk']} D={c['d']}, "
+                        f"e4m3fn + fp32 per-64-key scales, {keys}-key partitions"
+                        f"{'' if split else ' (default partition policy)'}",
+            "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+            "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+        }
     return res
 
 
@@ -231,7 +236,7 @@ def main():
                    "seq_len": c["n"], "head_dim": c["d"], "causal": True, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": _traffic_bytes(), "kernel": "attn_tile_kernel<128,BF16,BF16,4,64,false>",
+                     "traffic": _traffic_bytes(), "kernel": "attn_fwd_kernel<128,BF16>",
                      "kernel_ms": round(ev * 1e3, 4)},
     }
     if not a.no_decode:

@@ -8,6 +8,8 @@
 //   ds_read_b64_tr_b16: in each 16-lane group, lane i receives element (i%4) of the
 //                       8-byte rows addressed by lanes (i/4) + 4e, e = 0..3.
 //   v_permlane32_swap(x, x): {r0, r1} with max(r0, r1) = max(x[l], x[l^32]).
+//   ds_read_b64_tr_b8:  in each 16-lane group, lane i receives byte (i%8) of the
+//                       8-byte rows addressed by lanes (i%16)/8 + 2e, e = 0..7.
 //   v_cvt_pk_f32_fp8: OCP float8_e4m3fn -> fp32, exact for all 256 codes.
 #pragma once
 
@@ -24,6 +26,7 @@ typedef float f32x16 __attribute__((__vector_size__(64)));
 typedef float f32x4 __attribute__((__vector_size__(16)));
 typedef float f32x2 __attribute__((__vector_size__(8)));
 typedef short i16x4 __attribute__((__vector_size__(8)));
+typedef int i32x2 __attribute__((__vector_size__(8)));
 typedef uint32_t u32x4 __attribute__((__vector_size__(16)));
 typedef uint32_t u32x2 __attribute__((__vector_size__(8)));
 
@@ -171,6 +174,21 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   typedef i16x4 __attribute__((address_space(3))) * lds_v4_ptr;
   typedef uint16_t __attribute__((address_space(3))) * lds_u16_ptr;
   const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4_ptr)((lds_u16_ptr)p));
+  return __builtin_bit_cast(u32x2, r);
+#else
+  (void)p;
+  return u32x2{0, 0};
+#endif
+}
+
+// 8-byte transposed LDS read of 8-bit elements (ds_read_b64_tr_b8).  Within each
+// group of 16 lanes, lane i receives byte i % 8 of the 8-byte pieces addressed by
+// lanes (i % 16) / 8 + 2e of its group, e = 0..7, in order of e.
+__device__ __forceinline__ u32x2 lds_read_tr8(const uint8_t* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef i32x2 __attribute__((address_space(3))) * lds_v2_ptr;
+  typedef uint8_t __attribute__((address_space(3))) * lds_u8_ptr;
+  const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2_ptr)((lds_u8_ptr)p));
   return __builtin_bit_cast(u32x2, r);
 #else
   (void)p;

@@ -30,6 +30,7 @@ struct TileArgs {
   int32_t nq, nk;  // dense lengths; varlen: maxima
   int32_t n_rowblk;
   int32_t n_split, split_len;
+  int32_t ppw, n_chunk;  // split-K: partitions per workgroup, workgroups per (b, kv-head, row block)
   int32_t total;  // workgroups in the grid
   float qk_scale; // softmax scale * log2(e)
   int32_t causal;

@@ -1,0 +1,590 @@
+// Split-K flash-decoding kernels for MI355X (gfx950).
+//
+//   * attn_splitk_kernel: the reference's _attn_splitk_kernel
+//     (fused_attn/triton_splitk.py:29-96), including the FP8 K/V variant of
+//     _attn_fp8_kernel (fused_attn/fp8.py:59-122): un-normalised fp32 partial
+//     outputs plus (max, sum) statistics in the log2 domain, one per key partition;
+//   * splitk_combine_kernel: the log-sum-exp merge of the partitions
+//     (_splitk_combine_kernel, fused_attn/triton_splitk.py:99-127).
+//
+// Work decomposition.  Keys are cut into partitions of split_len keys (the unit the
+// partials and the combine work on).  A workgroup streams `ppw` consecutive
+// partitions of one (batch, kv-head) through LDS and writes one partial per
+// partition, so the fixed cost of a workgroup (Q fragments, the first tile's memory
+// latency) is paid once per ppw partitions and the global->LDS pipeline runs across
+// partition boundaries without a drain.
+//
+// A workgroup has NW waves; wave w owns 32 "rows", a row being a (q-head of the kv
+// group, query) pair, so the G = Hq/Hkv heads that share a kv-head read each K/V
+// tile once.  Per tile, per wave (S^T orientation, so the softmax is lane-local):
+//   S^T = K Q^T   v_mfma_f32_32x32x16: A = K rows from LDS, B = Q from VGPRs.
+//                 The C fragment gives each lane one row and 16 keys; the A-row ->
+//                 key map (kperm) hands each lane 8 contiguous keys per 16-key step.
+//   softmax       online, base 2, scale*log2(e) folded in; max/sum need only the
+//                 partner lane l^32 (v_permlane32_swap).
+//   P^T           rounded to 16 bits in place: the B operand of the next MFMA.
+//   O^T += V^T P^T  A = V^T read from row-major LDS with ds_read_b64_tr_b16.
+// K/V go global -> LDS by DMA (buffer_load ... lds) in their storage type; FP8 K/V
+// stay 8-bit in LDS (half the LDS per stage, so more workgroups per CU) and are
+// widened to 16 bits when read as MFMA operands, V through ds_read_b64_tr_b8.
+#include <float.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "fa_device.hpp"
+#include "fa_internal.hpp"
+#include "fa_tile.hpp"
+
+namespace fa {
+
+template <int D, class E, class KV, int NW, int BN>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) attn_splitk_kernel(const TileArgs a) {
+  using Shape = TileShape<D, BN>;    // 16-bit tiles
+  using Shape8 = TileShape8<D, BN>;  // FP8 tiles
+  constexpr bool IS_FP8 = KV::bytes == 1;
+  constexpr int TILE_BYTES = BN * D * KV::bytes;  // one K (or V) tile
+  constexpr int KB = BN / 32;   // 32-key MFMA blocks per tile
+  constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
+  constexpr int DB = D / 32;    // 32-wide d blocks of O^T
+  // one DMA wave instruction fills 1 KiB = 64 lanes x 16 B
+  constexpr int QPW = (TILE_BYTES / 1024) / NW;
+  static_assert(BN % 32 == 0 && D % 32 == 0 && (D == 64 || D == 128), "tile shape");
+  static_assert(TILE_BYTES % (1024 * NW) == 0, "tile loads must split evenly over the waves");
+  constexpr float NEG_INF = -__builtin_inff();
+
+  // Two LDS stages (K tile, then V tile) as separate arrays: every access names its
+  // stage at compile time, so the compiler can tell that the DMA filling one stage
+  // never aliases reads of the other (and does not wait for the prefetch before
+  // reading the current tile).
+  __shared__ __align__(16) uint8_t lds_st0[2 * TILE_BYTES];
+  __shared__ __align__(16) uint8_t lds_st1[2 * TILE_BYTES];
+
+  // ---- work item: (batch, kv-head, chunk of ppw partitions, row block) -------------
+  const int logical = xcd_remap((int)blockIdx.x, a.total);
+  const int rb = logical % a.n_rowblk;
+  int item = logical / a.n_rowblk;
+  const int chunk = item % a.n_chunk;
+  item /= a.n_chunk;
+  const int kvh = item % a.hkv;
+  const int b = item / a.hkv;
+
+  const int seq_q = a.nq, seq_k = a.nk;
+  const int R = a.group * seq_q;  // rows: (q-head in group, query)
+  const int r0 = rb * NW * 32;    // < R: the grid has ceil(R / (NW * 32)) row blocks
+  const int offset = seq_k - seq_q;  // bottom-right causal alignment (reference.py:24-33)
+
+  const int part0 = chunk * a.ppw;
+  const int part_end = min(part0 + a.ppw, a.n_split);
+  const int klo = part0 * a.split_len;
+  int khi = min(seq_k, part_end * a.split_len);
+  if (a.causal) {
+    // last query of the block (rows wrap around the queries once per q-head)
+    const int re = min(r0 + NW * 32, R);
+    const int qmax = (re - r0 >= seq_q || (r0 % seq_q) > ((re - 1) % seq_q)) ? seq_q - 1 : (re - 1) % seq_q;
+    khi = min(khi, qmax + offset + 1);
+  }
+  const int n_tiles = khi > klo ? (khi - klo + BN - 1) / BN : 0;
+  const int tiles_per_part = a.split_len / BN;  // split_len is a multiple of 64 (C ABI)
+
+  // ---- lane roles ------------------------------------------------------------------
+  const int tid = (int)threadIdx.x;
+  // wave index is uniform per wave: keep it (and every per-wave bound) in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int g = lane >> 5, j = lane & 31;
+  const int wr0 = r0 + wave * 32;
+  const int row = wr0 + j;
+  const bool row_ok = row < R;
+  const bool wave_active = wr0 < R;
+  const int hq = kvh * a.group + (row_ok ? row / seq_q : 0);
+  const int qi = row_ok ? row % seq_q : 0;
+  // Keys visible to every row of the wave need no element-wise mask; keys at or
+  // beyond wave_khi are visible to no row of the wave.
+  int wave_khi = khi, mask_from = khi;
+  if (a.causal && wave_active) {
+    const int we = min(wr0 + 32, R);
+    int qlo, qhi;
+    if (we - wr0 >= seq_q || (wr0 % seq_q) > ((we - 1) % seq_q)) {
+      qlo = 0;
+      qhi = seq_q - 1;
+    } else {
+      qlo = wr0 % seq_q;
+      qhi = (we - 1) % seq_q;
+    }
+    wave_khi = min(khi, qhi + offset + 1);
+    mask_from = min(khi, qlo + offset + 1);
+  }
+
+  // K/V of this (batch, kv-head), read with buffer loads: a load past the
+  // resource's byte limit returns zeros, which zero-fills the keys >= khi of the
+  // last tile without branches (masked keys must not carry NaN/Inf into P*V).
+  const uint8_t* kbase = (const uint8_t*)a.k + ((int64_t)b * a.skb + (int64_t)kvh * a.skh) * KV::bytes;
+  const uint8_t* vbase = (const uint8_t*)a.v + ((int64_t)b * a.svb + (int64_t)kvh * a.svh) * KV::bytes;
+  const int64_t krow_bytes = a.skn * KV::bytes, vrow_bytes = a.svn * KV::bytes;
+  const float* ksc = nullptr;
+  const float* vsc = nullptr;
+  if (KV::bytes == 1) {
+    ksc = a.k_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
+    vsc = a.v_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
+  }
+
+  // A negative softmax scale is applied by negating Q (exact for 16-bit floats),
+  // so the kernel always works with c = |scale| * log2(e) > 0 and max(c*s) = c*max(s).
+  // c is kept away from 0 so that a masked score (-inf) times c stays -inf; for a
+  // zero scale every 2^(c*s) is then 1 to float precision, as for c = 0.
+  const uint32_t qsign = a.qk_scale < 0.f ? 0x80008000u : 0u;
+  const float c_abs = fmaxf(fabsf(a.qk_scale), kMinScale);
+
+  // ---- Q fragments (B operand of S^T), resident for the whole kernel -------------
+  // (rows past the end read row 0 of the item, which exists, and are then zeroed:
+  // the loads stay unconditional and are all in flight together)
+  u32x4 qf[KS];
+  {
+    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + (int64_t)qi * a.sqn + 8 * g;
+    const uint32_t keep = row_ok ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = (ld16(qp + 16 * s) ^ qsign) & keep;
+  }
+
+  // ---- K/V tiles: global -> LDS (K rows permuted by kperm) ---------------------------
+  auto resources = [&](int n0, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv) {
+    // Byte limit = end of the tile's last key below khi.  It fits 32 bits (BN * row
+    // bytes < 2^31, checked at the C ABI) and is wave-uniform, so the descriptor lives
+    // in SGPRs.  Valid for any row stride, including 0 for a single-key cache.
+    const int valid = min(khi - n0, BN);
+    const uint32_t klim = __builtin_amdgcn_readfirstlane(
+        valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)krow_bytes + (uint32_t)(D * KV::bytes) : 0u);
+    const uint32_t vlim = __builtin_amdgcn_readfirstlane(
+        valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)vrow_bytes + (uint32_t)(D * KV::bytes) : 0u);
+    rk = make_rsrc(kbase + (int64_t)n0 * krow_bytes, klim);
+    rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, vlim);
+  };
+  // Each wave fills QPW 1-KiB blocks of the K and of the V tile straight from memory.
+  auto load_tile = [&](int n0, uint8_t* stage) {
+    __amdgpu_buffer_rsrc_t rk, rv;
+    resources(n0, rk, rv);
+    uint8_t* kl = stage;
+    uint8_t* vl = stage + TILE_BYTES;
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+      const int blk = wave * QPW + i;
+      const int byte = blk * 1024 + lane * 16;
+      const int r = byte / (D * KV::bytes), p = (byte % (D * KV::bytes)) / 16;
+      const int sk = IS_FP8 ? Shape8::swz_k(r) : Shape::swz_k(r);
+      const int sv = IS_FP8 ? Shape8::swz_v(r) : Shape::swz_v(r);
+      lds_dma16<true>(rk, kl + blk * 1024, kperm(r) * (int)krow_bytes + ((p ^ sk) * 16));
+      lds_dma16<true>(rv, vl + blk * 1024, r * (int)vrow_bytes + ((p ^ sv) * 16));
+    }
+  };
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+  // Running max m_run (log2 domain, scaled) and this lane's share of the row sum,
+  // both for the current partition.
+  float m_run = NEG_INF, l_run = 0.f;
+
+  // Per-lane LDS element offsets (within a stage) of the MFMA operand reads.
+  // K: S^T A-operand, row kb*32 + j, logical chunk 2s + g.
+  int koffs[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) koffs[s] = j * D + (((2 * s + g) ^ Shape::swz_k(j)) * 8);
+  // V: ds_read_b64_tr_b16 sources, rows 8g + 4*hi + (i >> 2) of each 16-key step,
+  // columns 32d + 16dh + 4(i & 3); the row term kb*32 + 16h is a constant offset.
+  const int tr_i = lane & 15, tr_dh = (lane >> 4) & 1;
+  int voffs[DB][2];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+      const int vr_row = 8 * g + 4 * hi + (tr_i >> 2);
+      const int col = 32 * d + 16 * tr_dh + 4 * (tr_i & 3);
+      voffs[d][hi] = vr_row * D + (((col >> 3) ^ Shape::swz_v(vr_row)) * 8) + (col & 7);
+    }
+  }
+  // FP8 tiles (byte offsets).  K: A-operand row j, 8 bytes at d = 16s + 8g.
+  int koffs8[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) koffs8[s] = j * D + ((s ^ Shape8::swz_k(j)) * 16) + 8 * g;
+  // V: ds_read_b64_tr_b8 sources.  Lane p of 16-lane group G points at row
+  // 8(G/2) + (p%16)/2 of the 16-key step, bytes 32d + 16(G%2) + 8(p%2), so that lane l
+  // receives keys 8(l/32) + 0..7 of d = 32d + l%32: the A layout of O^T += V^T P^T.
+  int voffs8[DB];
+  {
+    const int grp = lane >> 4, r8 = 8 * (grp >> 1) + ((lane & 15) >> 1);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) voffs8[d] = r8 * D + (((2 * d + (grp & 1)) ^ Shape8::swz_v(r8)) * 16) + 8 * (lane & 1);
+  }
+  const int qlim = qi + offset;  // last key this lane's row may see (causal)
+
+  // Un-normalised partial + log2-domain statistics of partition `part`
+  // (triton_splitk.py:90-96), then the state restarts for the next partition.
+  auto emit_partial = [&](int part) __attribute__((always_inline)) {
+    const float l_tot = sum_xor32(l_run);  // each lane summed its 16 of the row's keys per tile
+    if (wave_active && row_ok) {
+      const int64_t prow = ((int64_t)(b * a.hq + hq) * seq_q + qi) * a.n_split + part;
+      float* op = (float*)a.o + prow * D;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d0 = d * 32 + 8 * rq + 4 * g;
+          st16(op + d0, __builtin_bit_cast(u32x4, f32x4{oacc[d][4 * rq], oacc[d][4 * rq + 1], oacc[d][4 * rq + 2],
+                                                        oacc[d][4 * rq + 3]}));
+        }
+      }
+      if (g == 0) st8(a.ml + prow * 2, __builtin_bit_cast(u32x2, f32x2{m_run, l_tot}));
+    }
+#pragma unroll
+    for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+    m_run = NEG_INF;
+    l_run = 0.f;
+  };
+
+  if (n_tiles > 0) load_tile(klo, lds_st0);
+  lds_dma_wait();
+  __syncthreads();
+
+  // One tile: prefetch tile t+1 into the other stage, then S^T, softmax, O += P V on
+  // this stage.  The stage is a compile-time choice (the loop below is unrolled by 2).
+  auto tile_step = [&](auto stage_tag, int t) {
+    constexpr int ST = decltype(stage_tag)::value;
+    uint8_t* cur = ST == 0 ? lds_st0 : lds_st1;
+    uint8_t* nxt = ST == 0 ? lds_st1 : lds_st0;
+    const int n0 = klo + t * BN;
+    if (t + 1 < n_tiles) load_tile(n0 + BN, nxt);  // released by the previous barrier
+
+    if (wave_active && n0 < wave_khi) {
+      const uint8_t* Ks = cur;
+      const uint8_t* Vs = cur + TILE_BYTES;
+      // MFMA A operands from LDS (FP8 widened to E on the way)
+      auto k_operand = [&](int kb, int s) __attribute__((always_inline)) {
+        if constexpr (IS_FP8) {
+          const u32x2 raw = ld8(Ks + kb * 32 * D + koffs8[s]);
+          const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
+          return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          return ld16((const uint16_t*)Ks + kb * 32 * D + koffs[s]);
+        }
+      };
+      auto v_operand = [&](int kb, int h, int d) __attribute__((always_inline)) {
+        if constexpr (IS_FP8) {
+          const u32x2 raw = lds_read_tr8(Vs + (kb * 32 + 16 * h) * D + voffs8[d]);
+          const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
+          return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          const uint16_t* vp = (const uint16_t*)Vs + (kb * 32 + 16 * h) * D;
+          const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
+          const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
+          return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      };
+
+      // S^T = K Q^T.  The KB accumulation chains are independent; stepping them
+      // together keeps the MFMA pipe fed while each chain's last result is in flight.
+      f32x16 sacc[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sacc[kb] = f32x16{};
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32<E>(k_operand(kb, s), qf[s], sacc[kb]);
+      }
+      __builtin_amdgcn_s_setprio(0);
+
+      // per-block score scale (FP8: times the block's k_scale, fp8.py:104)
+      float sc[KB], vs[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if constexpr (KV::bytes == 1) {
+          const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
+          sc[kb] = fmaxf(c_abs * ksc[blk], kMinScale);
+          vs[kb] = vsc[blk];
+        } else {
+          sc[kb] = c_abs;
+          vs[kb] = 1.f;
+        }
+      }
+
+      // Masked tiles (the causal diagonal, the key tail) set excluded scores to -inf
+      // in one uniform block; exp2 then gives 0 for them, so the softmax below is the
+      // same straight-line code for every tile.
+      if (n0 + BN > mask_from) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+            const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
+            sacc[kb][r] = ok ? sacc[kb][r] : NEG_INF;
+          }
+        }
+      }
+
+      // tile max of the scaled scores (sc > 0: max of sc*s is sc*max(s))
+      float mt = NEG_INF;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        float mx = sacc[kb][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+        mt = fmaxf(mt, mx * sc[kb]);
+      }
+      mt = max_xor32(mt);
+
+      // Lazy rescale: keep the running max unless some row of the wave grew by
+      // more than 2^8; p = 2^(c*s - m_run) then stays <= 256 (no overflow risk),
+      // and O, l stay consistent because both use the same m_run.
+      const float m_new = fmaxf(m_run, mt);
+      if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
+        const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run - m_safe_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+        m_run = m_new;
+      }
+      const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
+
+      // P = 2^(c*s - m) as 16-bit B operands of PV
+      u32x4 pf[KB][2];
+      float rs = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(sacc[kb][r], sc[kb], -m_safe));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if constexpr (KV::bytes == 1) {
+            // v_scale folded into P (the reference scales P.V by v_scale, fp8.py:116)
+            const float v = vs[kb];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
+            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0] * v, p[8 * h + 1] * v), pack2<E>(p[8 * h + 2] * v, p[8 * h + 3] * v),
+                              pack2<E>(p[8 * h + 4] * v, p[8 * h + 5] * v), pack2<E>(p[8 * h + 6] * v, p[8 * h + 7] * v)};
+          } else {
+            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0], p[8 * h + 1]), pack2<E>(p[8 * h + 2], p[8 * h + 3]),
+                              pack2<E>(p[8 * h + 4], p[8 * h + 5]), pack2<E>(p[8 * h + 6], p[8 * h + 7])};
+            // the row sum of the rounded P that the MFMA consumes (so O/l is a convex combination)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rs = sum2<E>(pf[kb][h][e], rs);
+          }
+        }
+      }
+      l_run += rs;
+
+      // O^T += V^T P^T
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int d = 0; d < DB; ++d) {  // DB independent chains per 16-key step
+            oacc[d] = mfma32<E>(v_operand(kb, h, d), pf[kb][h], oacc[d]);
+          }
+        }
+      }
+      __builtin_amdgcn_s_setprio(0);
+    }
+    // the last tile of a partition closes it
+    if ((t + 1) % tiles_per_part == 0 || t + 1 == n_tiles) emit_partial(part0 + t / tiles_per_part);
+
+    if (t + 1 < n_tiles) lds_dma_wait();
+    __syncthreads();
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
+  }
+  // partitions past the visible keys (causal, or past the sequence end): empty
+  // partials, m = -inf and l = 0, which the combine weighs by zero
+  for (int part = part0 + (n_tiles + tiles_per_part - 1) / tiles_per_part; part < part_end; ++part) emit_partial(part);
+}
+
+// Log-sum-exp merge of split-K partials (triton_splitk.py:99-127):
+//   m = max_s m_s;  w_s = 2^(m_s - m);  O = sum_s w_s O_s / sum_s w_s l_s   (0 when the sum is 0)
+// One 256-thread workgroup per output row; D/4 threads cover a partial row with
+// float4 loads, so 256/(D/4) splits are read concurrently.
+template <int D, class E>
+__global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c) {
+  constexpr int TPS = D / 4;
+  constexpr int SPB = 256 / TPS;
+  constexpr float NEG_INF = -__builtin_inff();
+  __shared__ float red[256];
+  __shared__ f32x4 part[SPB][TPS];
+  __shared__ float lpart[SPB];
+
+  const int64_t row = blockIdx.x;  // (b, hq, qi) flattened
+  const int S = c.n_split;
+  const float* ml = c.ml + row * S * 2;
+  const float* op = c.opart + row * (int64_t)S * D;
+  const int tid = (int)threadIdx.x;
+
+  float m = NEG_INF;
+  for (int s = tid; s < S; s += 256) m = fmaxf(m, ml[2 * s]);
+  red[tid] = m;
+  __syncthreads();
+#pragma unroll
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+    __syncthreads();
+  }
+  const float mx = red[0];
+  const float m_safe = (mx == NEG_INF) ? 0.f : mx;
+
+  const int sg = tid / TPS, dq = tid % TPS;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+#pragma unroll 4
+  for (int s = sg; s < S; s += SPB) {
+    const f32x2 st = __builtin_bit_cast(f32x2, ld8(ml + 2 * s));
+    const float w = fast_exp2(st[0] - m_safe);
+    l += w * st[1];
+    acc += w * __builtin_bit_cast(f32x4, ld16(op + (int64_t)s * D + 4 * dq));
+  }
+  part[sg][dq] = acc;
+  if (dq == 0) lpart[sg] = l;
+  __syncthreads();
+  if (tid < TPS) {
+    f32x4 tot = part[0][tid];
+    float lt = lpart[0];
+#pragma unroll
+    for (int k = 1; k < SPB; ++k) {
+      tot += part[k][tid];
+      lt += lpart[k];
+    }
+    const float inv = 1.f / ((lt == 0.f) ? 1.f : lt);
+    const int qi = (int)(row % c.nq);
+    const int64_t bh = row / c.nq;
+    const int hq = (int)(bh % c.hq);
+    const int64_t b = bh / c.hq;
+    uint16_t* o = (uint16_t*)c.o + b * c.sob + (int64_t)hq * c.soh + (int64_t)qi * c.son + 4 * tid;
+    st8(o, u32x2{pack2<E>(tot[0] * inv, tot[1] * inv), pack2<E>(tot[2] * inv, tot[3] * inv)});
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Host-side launchers
+// ------------------------------------------------------------------------------------
+
+template <int D, class E, class KV, int NW, int BN>
+static hipError_t launch_splitk(const TileArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_splitk_kernel<D, E, KV, NW, BN>), dim3((unsigned)a.total), dim3(NW * 64), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int D, class E>
+static hipError_t launch_combine(const CombineArgs& c, int64_t rows, hipStream_t stream) {
+  hipLaunchKernelGGL((splitk_combine_kernel<D, E>), dim3((unsigned)rows), dim3(256), 0, stream, c);
+  return hipGetLastError();
+}
+
+TileArgs common_args(const fa_fwd_params& p) {
+  TileArgs a{};
+  a.q = p.q;
+  a.k = p.k;
+  a.v = p.v;
+  a.sqb = p.q_stride_b;
+  a.sqh = p.q_stride_h;
+  a.sqn = p.q_stride_n;
+  a.skb = p.k_stride_b;
+  a.skh = p.k_stride_h;
+  a.skn = p.k_stride_n;
+  a.svb = p.v_stride_b;
+  a.svh = p.v_stride_h;
+  a.svn = p.v_stride_n;
+  a.hq = p.heads_q;
+  a.hkv = p.heads_kv;
+  a.group = p.heads_q / p.heads_kv;
+  a.nq = p.seqlen_q;
+  a.nk = p.seqlen_k;
+  a.qk_scale = p.scale * kLog2e;  // same fp32 product as triton_fwd.py:143
+  a.causal = p.causal ? 1 : 0;
+  a.k_scale = p.k_scale;
+  a.v_scale = p.v_scale;
+  a.ssb = p.scale_stride_b;
+  a.ssh = p.scale_stride_h;
+  return a;
+}
+
+int splitk_waves_for_rows(int rows) { return rows <= 32 ? 1 : (rows <= 64 ? 2 : 4); }
+
+// Partitions per workgroup.  One partition per workgroup measured fastest on MI355X
+// for 16-bit and FP8 caches (fine-grained workgroups keep every CU's memory pipeline
+// full to the end of the grid); several per workgroup only cap the grid at kMaxWgs.
+int splitk_parts_per_wg(int64_t items, int n_split) {
+  constexpr int64_t kMaxWgs = int64_t{1} << 20;
+  const int64_t want = (items * n_split + kMaxWgs - 1) / kMaxWgs;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(want, n_split));
+}
+
+template <int D, class E, class KV>
+static hipError_t launch_split_nw(const TileArgs& a, int nw, hipStream_t stream) {
+  switch (nw) {
+    case 1:
+      return launch_splitk<D, E, KV, 1, 32>(a, stream);
+    case 2:
+      return launch_splitk<D, E, KV, 2, 32>(a, stream);
+    default:
+      return launch_splitk<D, E, KV, 4, 64>(a, stream);
+  }
+}
+
+template <int D, class E>
+static hipError_t launch_split(const TileArgs& a, bool fp8, int nw, hipStream_t stream) {
+  return fp8 ? launch_split_nw<D, E, FP8>(a, nw, stream) : launch_split_nw<D, E, E>(a, nw, stream);
+}
+
+fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,
+                     const char** err) {
+  TileArgs a = common_args(p);
+  if (p.batch <= 0 || p.seqlen_q <= 0) return FA_OK;
+  const int S = p.seqlen_k > 0 ? (p.seqlen_k + split_len - 1) / split_len : 1;
+  const int rows = a.group * p.seqlen_q;
+  const int nw = splitk_waves_for_rows(rows);
+  a.n_rowblk = (rows + nw * 32 - 1) / (nw * 32);
+  a.n_split = S;
+  a.split_len = split_len;
+  const int64_t items = (int64_t)p.batch * p.heads_kv * a.n_rowblk;
+  a.ppw = splitk_parts_per_wg(items, S);
+  a.n_chunk = (S + a.ppw - 1) / a.ppw;
+  const int64_t total = items * a.n_chunk;
+  const int64_t out_rows = (int64_t)p.batch * p.heads_q * p.seqlen_q;
+  if (total > INT32_MAX || out_rows > INT32_MAX) {
+    *err = "grid too large";
+    return FA_ERR_UNSUPPORTED;
+  }
+  a.total = (int32_t)total;
+  a.o = workspace;
+  a.ml = (float*)workspace + out_rows * S * p.head_dim;
+  const bool fp8 = p.kv_dtype == FA_DTYPE_FP8_E4M3;
+  const bool bf = p.dtype == FA_DTYPE_BF16;
+  hipError_t e = hipErrorInvalidValue;
+  if (p.head_dim == 128) {
+    e = bf ? launch_split<128, BF16>(a, fp8, nw, stream) : launch_split<128, F16>(a, fp8, nw, stream);
+  } else if (p.head_dim == 64) {
+    e = bf ? launch_split<64, BF16>(a, fp8, nw, stream) : launch_split<64, F16>(a, fp8, nw, stream);
+  }
+  if (e != hipSuccess) return hip_status(e, err);
+
+  CombineArgs c{};
+  c.opart = (const float*)a.o;
+  c.ml = a.ml;
+  c.o = p.o;
+  c.sob = p.o_stride_b;
+  c.soh = p.o_stride_h;
+  c.son = p.o_stride_n;
+  c.hq = p.heads_q;
+  c.nq = p.seqlen_q;
+  c.n_split = S;
+  if (p.head_dim == 128) {
+    e = bf ? launch_combine<128, BF16>(c, out_rows, stream) : launch_combine<128, F16>(c, out_rows, stream);
+  } else {
+    e = bf ? launch_combine<64, BF16>(c, out_rows, stream) : launch_combine<64, F16>(c, out_rows, stream);
+  }
+  return hip_status(e, err);
+}
+
+}  // namespace fa

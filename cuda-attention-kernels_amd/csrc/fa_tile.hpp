@@ -30,3 +30,23 @@ struct TileShape {
 __device__ __forceinline__ constexpr int kperm(int r) { return (r & ~0xC) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
 }  // namespace fa
+
+namespace fa {
+
+// FP8 K/V tiles: [BN rows][D bytes], raw e4m3fn as loaded, 16-byte chunks
+// XOR-swizzled per row.  64 banks x 4 bytes = 256 bytes hold 256 / D rows.
+template <int D, int BN>
+struct TileShape8 {
+  static constexpr int CPR = D / 16;             // 16-byte chunks per row
+  static constexpr int ROWS_PER_256B = 256 / D;  // rows sharing one 256-byte bank line
+  static constexpr int TILE = BN * D;            // bytes per K (or V) tile
+  // K is read 8 bytes per lane, 32 rows at one logical chunk: rows of one bank line
+  // position get distinct chunks (two lanes share a bank pair at most).
+  __device__ static constexpr int swz_k(int row) { return (row / ROWS_PER_256B) % CPR; }
+  // V is read with ds_read_b64_tr_b8: 8 consecutive rows at one chunk per 16 lanes,
+  // the chunk's parity differing between the two 16-lane halves of 32 lanes.  Even
+  // XOR values keep the parities apart and spread the 8 rows over distinct banks.
+  __device__ static constexpr int swz_v(int row) { return 2 * ((row / ROWS_PER_256B) % (CPR / 2)); }
+};
+
+}  // namespace fa

@@ -77,7 +77,12 @@ def attention_fp8(
         return attention_reference(q, dequantize_kv_fp8(k8, k_scale), dequantize_kv_fp8(v8, v_scale),
                                    causal=causal, scale=scale)
     if split_len is None:
-        split_len = 128 if q.shape[-2] <= 16 else max(QBLOCK, -(-k8.shape[-2] // QBLOCK) * QBLOCK)
+        if q.shape[-2] <= 16:  # decode-shaped: partitions sized for the grid (ops.default_split_len)
+            from .ops import default_split_len
+
+            split_len = default_split_len(q.shape[-2], k8.shape[-2], q.shape[0], k8.shape[1], q.shape[1] // k8.shape[1])
+        else:  # prefill-shaped: one partition, as the reference's single-pass kernel (fp8.py:136-145)
+            split_len = max(QBLOCK, -(-k8.shape[-2] // QBLOCK) * QBLOCK)
     return _hip.splitk(q, k8, v8, causal=causal, scale=scale, split_len=int(split_len), k_scale=k_scale,
                        v_scale=v_scale)
 

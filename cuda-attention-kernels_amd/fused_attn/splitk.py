@@ -60,7 +60,7 @@ def attention_splitk(
         else:
             from .ops import default_split_len
 
-            split_len = default_split_len(q.shape[-2], n_k)
+            split_len = default_split_len(q.shape[-2], n_k, q.shape[0], k.shape[1], q.shape[1] // k.shape[1])
     return _hip.splitk(q, k, v, causal=causal, scale=scale, split_len=int(split_len))
 
 

@@ -86,5 +86,8 @@ def test_baseline_decode_configs(n_q, causal):
     err = max_err(out, ref)
     print(f"max_abs_err={err:.3e}", flush=True)
     assert err <= TOL[torch.bfloat16]
-    # the public op picks split-K for this shape and gives the same bits
-    assert torch.equal(fused_attn.attention(q, k, v, causal=causal), out)
+    # the public op picks split-K for this shape, with the default partition length
+    split = ops.default_split_len(n_q, 32768, 32, 8, 4)
+    op_out = fused_attn.attention(q, k, v, causal=causal)
+    assert torch.equal(op_out, fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split))
+    assert max_err(op_out, ref) <= TOL[torch.bfloat16]
