@@ -93,7 +93,7 @@ def bench_prefill(steps, warmup):
     return flops, wall, ev
 
 
-def bench_decode(steps, warmup):
+def bench_decode(steps, warmup, only_128=False):
     import torch
 
     import fused_attn
@@ -103,7 +103,8 @@ def bench_decode(steps, warmup):
     g = torch.Generator(device="cuda").manual_seed(0)
     k = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
     v = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
-    for nq, causal, split in ((1, False, 128), (16, True, 128), (1, False, None), (16, True, None)):
+    cases = ((1, False, 128),) if only_128 else ((1, False, 128), (16, True, 128), (1, False, None), (16, True, None))
+    for nq, causal, split in cases:
         q = torch.randn(c["b"], c["hq"], nq, c["d"], device="cuda", generator=g).bfloat16()
         fn = lambda: fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split)  # noqa: E731
         wall, ev = _time_calls(fn, steps, warmup)
@@ -120,6 +121,8 @@ def bench_decode(steps, warmup):
         }
     del k, v
     torch.cuda.empty_cache()
+    if only_128:
+        return res
     c = FP8_DECODE
     q = torch.randn(c["b"], c["hq"], 1, c["d"], device="cuda", generator=g).bfloat16()
     k8, ks = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
@@ -186,8 +189,8 @@ def run_only(which, steps, warmup):
     if which == "prefill":
         flops, wall, ev = bench_prefill(steps, warmup)
         print(f"prefill: {flops / ev / 1e12:.1f} TFLOP/s kernel, {ev * 1e3:.4f} ms", flush=True)
-    elif which == "decode":
-        print(json.dumps(bench_decode(steps, warmup)), flush=True)
+    elif which in ("decode", "decode128"):
+        print(json.dumps(bench_decode(steps, warmup, only_128=which == "decode128")), flush=True)
     else:
         wall, ev, nbytes = copy_calibration(steps, warmup)
         print(f"copy {nbytes} B: {ev * 1e3:.4f} ms, {2 * nbytes / ev / 1e9:.1f} GB/s read+write", flush=True)
@@ -200,7 +203,7 @@ def main():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
-    p.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+    p.add_argument("--only", choices=["prefill", "decode", "decode128", "copy"], default=None,
                    help="run one workload without the JSON line (for profiler runs)")
     a = p.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

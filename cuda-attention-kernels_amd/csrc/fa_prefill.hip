@@ -57,19 +57,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   __shared__ __align__(16) uint16_t v_buf1[TILE];
 
   // ---- work item: (batch, q-head, 128-query block) -----------------------------------
-  // xcd_remap hands each of the 8 XCDs a contiguous range of logical indices.  The
-  // (batch, q-head) pairs are cut into 8 groups, one per range, so that an XCD's L2
-  // sees the K/V of few kv-heads; within a group the query blocks are ordered by
-  // rank (heaviest causal blocks first), all heads of the group at each rank, which
-  // balances the XCD's CUs.
+  // Scheduling units: the q-heads of as many kv-heads as keep about kL2UnitBytes of
+  // K/V (one XCD's L2 is 4 MB).  Units follow each other in logical order, and
+  // xcd_remap hands each XCD a contiguous range of logical indices, so an XCD works
+  // through one or two units at a time and re-reads K/V from its L2.  Inside a unit
+  // the query blocks go by rank, heaviest causal blocks first, all heads of the unit
+  // at each rank, which keeps the XCD's CUs evenly loaded to the end.
+  constexpr int64_t kL2UnitBytes = int64_t{4} << 20;
   const int logical = xcd_remap((int)blockIdx.x, a.total);
   const int nbh = a.total / a.n_rowblk;  // (batch, q-head) pairs
-  const int grp_heads = (nbh + 7) / 8;
-  const int grp = logical / (grp_heads * a.n_rowblk);
-  const int within = logical % (grp_heads * a.n_rowblk);
-  const int grp_size = min(grp_heads, nbh - grp * grp_heads);
-  const int mrev = within / grp_size;
-  int item = grp * grp_heads + within % grp_size;
+  const int64_t kv_head_bytes = (int64_t)max(a.nk, 1) * D * 2 * 2;
+  const int unit_heads = max(1, (int)(kL2UnitBytes / kv_head_bytes)) * a.group;
+  const int unit = logical / (unit_heads * a.n_rowblk);
+  const int within = logical % (unit_heads * a.n_rowblk);
+  const int unit_size = min(unit_heads, nbh - unit * unit_heads);
+  const int mrev = within / unit_size;
+  int item = unit * unit_heads + within % unit_size;
   const int gi = item % a.group;
   item /= a.group;
   const int kvh = item % a.hkv;
