@@ -152,7 +152,7 @@ __device__ __forceinline__ void lds_dma_wait() {
 // raised, and O rescaled, once a row's max grows by more than this.
 constexpr float kRescaleLog2 = 8.0f;
 
-// Smallest score multiplier the kernels use (see the c_abs comment in the tile kernel).
+// Smallest score multiplier the kernels use: a masked score (-inf) times it stays -inf.
 constexpr float kMinScale = 1e-30f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

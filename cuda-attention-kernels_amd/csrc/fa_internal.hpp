@@ -1,5 +1,5 @@
 // Internal interface between the C ABI (fa_abi.cpp) and the kernel launchers
-// (fa_kernels.hip).  Not part of the public header.
+// (fa_prefill.hip, fa_splitk.hip).  Not part of the public header.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -10,7 +10,7 @@
 
 namespace fa {
 
-// Kernel arguments of the FA2 tile kernel, passed by value.  Pointers are raw
+// Kernel arguments of the prefill and split-K kernels, passed by value.  Pointers are raw
 // device pointers; strides are in elements of the pointed-to type.
 struct TileArgs {
   const void* q;

@@ -7,7 +7,7 @@
 // A workgroup of 4 waves covers 128 queries of one q-head; wave w owns 32 of
 // them.  K and V stream through LDS in 64-key tiles, each in two buffers filled
 // straight from memory (buffer_load ... lds).  The product order per wave is the
-// same as in the split-K tile kernel (S^T = K Q^T with the softmax lane-local,
+// same as in the split-K kernel (S^T = K Q^T with the softmax lane-local,
 // P^T kept in VGPRs as the B operand of O^T += V^T P^T), but the loop is
 // software-pipelined so that one wave always has matrix work and vector work
 // that do not depend on each other:
