@@ -64,7 +64,6 @@ fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok) {
       return fail(FA_ERR_INVALID_ARGUMENT, "varlen needs cu_seqlens_q and cu_seqlens_k");
     if (p->max_seqlen_q < 0 || p->max_seqlen_k < 0)
       return fail(FA_ERR_INVALID_ARGUMENT, "max_seqlen must be non-negative");
-    if (p->lse != nullptr) return fail(FA_ERR_UNSUPPORTED, "LSE output is not available on the varlen path");
   }
   const bool empty = p->batch == 0 || (varlen ? p->max_seqlen_q == 0 : p->seqlen_q == 0);
   if (empty) return FA_OK;
@@ -110,6 +109,7 @@ fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream) {
   g_last_error.clear();
   fa_status st = validate(p, /*varlen=*/true, /*fp8_ok=*/false);
   if (st != FA_OK) return st;
+  if (p->lse != nullptr && p->lse_stride_h < 0) return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
   const char* err = nullptr;
   st = fa::run_fwd(*p, true, reinterpret_cast<hipStream_t>(stream), &err);
   if (st != FA_OK) return fail(st, err ? err : "launch failed");

@@ -381,7 +381,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   }
   if (a.lse != nullptr && g == 0) {
     // natural-log LSE (triton_fwd.py:169-172)
-    a.lse[(int64_t)b * a.slb + (int64_t)hq * a.slh + qi] = (m_run + __log2f(l_safe)) * kLn2;
+    a.lse[(int64_t)b * a.slb + (int64_t)hq * a.slh + (qtok0 + qi)] = (m_run + __log2f(l_safe)) * kLn2;
   }
 }
 
@@ -406,7 +406,7 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
     a.cu_k = p.cu_seqlens_k;
     a.nq = p.max_seqlen_q;
     a.nk = p.max_seqlen_k;
-    a.sqb = a.skb = a.svb = a.sob = 0;
+    a.sqb = a.skb = a.svb = a.sob = a.slb = 0;  // rows are addressed by packed token index
   }
   if (a.nq <= 0 || p.batch <= 0) return FA_OK;
   a.n_rowblk = (a.nq + 127) / 128;

@@ -388,11 +388,12 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
       }
       __builtin_amdgcn_s_setprio(0);
     }
-    // the last tile of a partition closes it
-    if ((t + 1) % tiles_per_part == 0 || t + 1 == n_tiles) emit_partial(part0 + t / tiles_per_part);
-
     if (t + 1 < n_tiles) lds_dma_wait();
     __syncthreads();
+    // The last tile of a partition closes it.  Its stores are issued after this
+    // tile's wait: vmcnt counts stores too, so they complete under the next tile
+    // instead of stalling this one.
+    if ((t + 1) % tiles_per_part == 0 || t + 1 == n_tiles) emit_partial(part0 + t / tiles_per_part);
   };
   for (int t = 0; t < n_tiles; t += 2) {
     tile_step(std::integral_constant<int, 0>{}, t);

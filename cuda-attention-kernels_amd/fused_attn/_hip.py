@@ -306,8 +306,11 @@ def fwd(q, k, v, causal: bool = False, scale: Optional[float] = None, return_lse
 
 
 def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int, causal: bool = False,
-               scale: Optional[float] = None, out: Optional[torch.Tensor] = None):
-    """Packed varlen forward.  q [Tq,Hq,D]; k, v [Tk,Hkv,D]; cu_seqlens int32 [nseq+1] on the GPU."""
+               scale: Optional[float] = None, out: Optional[torch.Tensor] = None, return_lse: bool = False):
+    """Packed varlen forward.  q [Tq,Hq,D]; k, v [Tk,Hkv,D]; cu_seqlens int32 [nseq+1] on the GPU.
+
+    With ``return_lse`` also returns the natural-log LSE as fp32 [Hq, Tq]; rows of tokens outside every
+    sequence are left unwritten (like the output rows)."""
     _require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k)
     if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
         raise RuntimeError("cu_seqlens must be int32")
@@ -318,11 +321,15 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqle
     q, k, v = _prep_qkv(q, k, v)
     cu_q, cu_k = cu_seqlens_q.contiguous(), cu_seqlens_k.contiguous()
     o = _new_output(q) if out is None else out
+    lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device) if return_lse else None
     p = make_params(q, k, v, o, causal, scale, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=max_seqlen_q,
                     max_seqlen_k=max_seqlen_k)
+    if lse is not None:  # [Hq, Tq]: head stride Tq, unit token stride
+        p.lse = lse.data_ptr()
+        p.lse_stride_b, p.lse_stride_h = 0, lse.stride(0)
     with torch.cuda.device(q.device):
         _check(lib.fa_attention_varlen_fwd(ctypes.byref(p), ctypes.c_void_p(_stream(q))), "attention_varlen_fwd")
-    return o
+    return (o, lse) if return_lse else o
 
 
 def split_len_for(seqlen_k: int, num_splits: int, block: int = FP8_QBLOCK) -> int:

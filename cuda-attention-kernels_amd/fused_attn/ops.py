@@ -124,6 +124,7 @@ def default_split_len(seqlen_q: int, seqlen_k: int, batch: int = 1, heads_kv: in
     return int(min(max(keys, DEFAULT_SPLIT_KEYS), MAX_SPLIT_KEYS))
 
 
+@torch.library.custom_op("fused_attn::attention_varlen", mutates_args=())
 def attention_varlen(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -137,13 +138,21 @@ def attention_varlen(
 ) -> torch.Tensor:
     """Packed/ragged attention. q: [total_q, H_q, D]; k, v: [total_k, H_kv, D] (reference: ops.py:107-124).
 
-    On GPU tensors this runs the HIP kernel in varlen mode (the reference ran its
-    Python reference loop whenever its CUDA extension was built, ops.py:119-124).
+    Same signature as the reference's plain function, registered as a custom op with a
+    fake so that ``torch.compile(fullgraph=True)`` traces it like ``attention``.  On GPU
+    tensors it runs the HIP kernel in varlen mode (the reference ran its Python
+    reference loop whenever its CUDA extension was built, ops.py:119-124).
     """
     if _pick_backend(q) == "hip":
         return _hip.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, causal=causal,
                                scale=scale)
     return attention_varlen_reference(q, k, v, cu_seqlens_q, cu_seqlens_k, causal=causal, scale=scale)
+
+
+@attention_varlen.register_fake
+def _attention_varlen_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, causal=False,
+                           scale=None):
+    return q.new_empty(q.shape)
 
 
 def pack_varlen(tensors: list[torch.Tensor]):

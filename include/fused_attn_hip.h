@@ -79,8 +79,9 @@ typedef struct fa_fwd_params {
   const int32_t* cu_seqlens_q;
   const int32_t* cu_seqlens_k;
   int32_t max_seqlen_q, max_seqlen_k;
-  /* optional natural-log LSE output [B, Hq, Nq] fp32 (NULL = not written);
-     reference: WRITE_LSE in fused_attn/triton_fwd.py:169-172 */
+  /* optional natural-log LSE output, fp32 (NULL = not written); reference: WRITE_LSE in
+     fused_attn/triton_fwd.py:169-172.  Dense: [B, Hq, Nq] at b*lse_stride_b + h*lse_stride_h + n.
+     Varlen: [Hq, total_q] at h*lse_stride_h + token (lse_stride_b unused); not on split-K. */
   float* lse;
   int64_t lse_stride_b, lse_stride_h;
   /* FP8 K/V block scales, fp32 [B, Hkv, ceil(Nk/64)] (fused_attn/fp8.py:31-45);
@@ -96,7 +97,7 @@ typedef struct fa_fwd_params {
 fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
 
 /* Packed variable-length forward.  Replaces attention_varlen_triton
-   (fused_attn/triton_fwd.py:268-309).  Needs cu_seqlens_q/k and max_seqlen_q. */
+   (fused_attn/triton_fwd.py:268-309).  Needs cu_seqlens_q/k and max_seqlen_q; optional LSE. */
 fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream);
 
 /* Bytes of workspace fa_attention_splitk needs for `num_splits` key partitions:

@@ -112,8 +112,11 @@ def test_varlen_validation(lib):
     assert "cu_seqlens" in lib.fa_last_error().decode()
     p = _params(cu_seqlens_q=0x20000, cu_seqlens_k=0x20000, max_seqlen_q=-1)
     assert lib.fa_attention_varlen_fwd(ctypes.byref(p), None) == _hip.FA_ERR_INVALID_ARGUMENT
-    p = _params(cu_seqlens_q=0x20000, cu_seqlens_k=0x20000, max_seqlen_q=8, max_seqlen_k=8, lse=0x30000)
-    assert lib.fa_attention_varlen_fwd(ctypes.byref(p), None) == _hip.FA_ERR_UNSUPPORTED
+    # LSE is accepted on the varlen path ([Hq, total_q]); a negative head stride is rejected
+    p = _params(cu_seqlens_q=0x20000, cu_seqlens_k=0x20000, max_seqlen_q=8, max_seqlen_k=8, lse=0x30000,
+                lse_stride_h=-1)
+    assert lib.fa_attention_varlen_fwd(ctypes.byref(p), None) == _hip.FA_ERR_INVALID_ARGUMENT
+    assert "LSE" in lib.fa_last_error().decode()
 
 
 def test_splitk_validation(lib):

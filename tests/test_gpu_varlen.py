@@ -83,3 +83,55 @@ def test_baseline_varlen_config():
     err = max_err(out, ref)
     print(f"lens={lens} max_abs_err={err:.3e}", flush=True)
     assert err <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("lens", [[5, 33, 70], [64, 0, 17], [1, 0, 130]])
+def test_varlen_lse(lens, causal):
+    """LSE [Hq, total_q] per packed token equals logsumexp of that sequence's scores; rows with no key are -inf."""
+    import math
+
+    announce(f"varlen lse lens={lens} causal={causal}")
+    torch.manual_seed(0)
+    h_q, h_kv, d = 8, 2, 128
+    qs = [randn(n, h_q, d, dtype=torch.bfloat16) for n in lens]
+    ks = [randn(n + 3, h_kv, d, dtype=torch.bfloat16) for n in lens]
+    q, cu_q, max_q = fused_attn.pack_varlen(qs)
+    k, cu_k, max_k = fused_attn.pack_varlen(ks)
+    out, lse = _hip.varlen_fwd(q, k, k, cu_q, cu_k, max_q, max_k, causal=causal, return_lse=True)
+    assert lse.shape == (h_q, q.shape[0]) and lse.dtype == torch.float32
+    assert torch.equal(out, fused_attn.attention_varlen(q, k, k, cu_q, cu_k, max_q, max_k, causal=causal))
+    got = lse.cpu()
+    cq, ck = cu_q.tolist(), cu_k.tolist()
+    for i in range(len(lens)):
+        nq, nk = cq[i + 1] - cq[i], ck[i + 1] - ck[i]
+        if nq == 0:
+            continue
+        qf = q[cq[i]:cq[i + 1]].float().cpu().transpose(0, 1)
+        kf = orc.expand_kv(k[ck[i]:ck[i + 1]].float().cpu().transpose(0, 1)[None], h_q // h_kv)[0]
+        s = torch.matmul(qf, kf.transpose(-1, -2)) / math.sqrt(d)
+        if causal:
+            s = s.masked_fill(~orc.causal_mask(nq, nk), float("-inf"))
+        ref = torch.logsumexp(s, dim=-1)
+        g = got[:, cq[i]:cq[i + 1]]
+        fin = torch.isfinite(ref)
+        assert torch.equal(fin, torch.isfinite(g))
+        # l sums the bf16-rounded P the MFMA consumes: bf16-level relative error in l
+        assert (g[fin] - ref[fin]).abs().max().item() < 2.0 ** -8
+
+
+def test_attention_triton_alias_gives_the_kernel_result():
+    from fused_attn.triton_fwd import attention_triton, attention_varlen_triton
+
+    announce("triton_fwd aliases")
+    torch.manual_seed(0)
+    q = randn(2, 8, 100, 128, dtype=torch.bfloat16)
+    k = randn(2, 2, 100, 128, dtype=torch.bfloat16)
+    o, lse = attention_triton(q, k, k, causal=True, return_lse=True)
+    o2, lse2 = _hip.fwd(q, k, k, causal=True, return_lse=True)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    qs = [randn(n, 8, 128, dtype=torch.bfloat16) for n in (3, 50)]
+    qp, cu, mx = fused_attn.pack_varlen(qs)
+    kp, cuk, mk = fused_attn.pack_varlen([randn(n, 2, 128, dtype=torch.bfloat16) for n in (3, 50)])
+    assert torch.equal(attention_varlen_triton(qp, kp, kp, cu, cuk, mx, mk, causal=True),
+                       fused_attn.attention_varlen(qp, kp, kp, cu, cuk, mx, mk, causal=True))

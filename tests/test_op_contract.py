@@ -29,6 +29,23 @@ def test_op_schema_matches_reference():
                       "float? scale=None) -> Tensor")
 
 
+def test_varlen_is_a_custom_op_with_fake():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    schema = str(torch.ops.fused_attn.attention_varlen.default._schema)
+    assert schema == ("fused_attn::attention_varlen(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, "
+                      "Tensor cu_seqlens_k, SymInt max_seqlen_q, SymInt max_seqlen_k, bool causal=False, "
+                      "float? scale=None) -> Tensor")
+    cu = torch.tensor([0, 3, 3, 10], dtype=torch.int32)
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        q = torch.empty(10, 4, 32, dtype=torch.bfloat16)
+        k = torch.empty(10, 2, 32, dtype=torch.bfloat16)
+        out = fused_attn.attention_varlen(q, k, k, cu, cu, 7, 7, True)
+    assert out.shape == (10, 4, 32) and out.dtype == torch.bfloat16
+    q, k, v = torch.randn(10, 4, 32), torch.randn(10, 2, 32), torch.randn(10, 2, 32)
+    torch.library.opcheck(fused_attn.attention_varlen, (q, k, v, cu, cu, 7, 7, True, None))
+
+
 def test_torch_compile_no_graph_break():
     torch._dynamo.reset()
 
@@ -135,3 +152,36 @@ def test_exports_match_reference_surface():
                  "quantize_kv_fp8", "dequantize_kv_fp8"):
         assert callable(getattr(fused_attn, name)), name
     assert fused_attn.__version__ == "0.3.0"
+
+
+def test_reference_import_paths():
+    """The reference's callers import these module paths (benchmarks/bench_decode.py:47-48,
+    tests/test_splitk_fp8.py:45); here they are HIP-backed."""
+    from fused_attn.triton_fwd import attention_triton, attention_varlen_triton
+    from fused_attn.triton_splitk import attention_splitk_triton, choose_num_splits
+
+    assert choose_num_splits(1, 8, 32768, 1, num_sms=108) == 27
+    q, k, v = torch.randn(1, 4, 9, 16), torch.randn(1, 2, 12, 16), torch.randn(1, 2, 12, 16)
+    ref = orc.attention(q, k, v, causal=True)
+    assert torch.allclose(attention_triton(q, k, v, causal=True), ref, atol=1e-5)
+    assert torch.allclose(attention_splitk_triton(q, k, v, causal=True), ref, atol=1e-5)
+    cu = torch.tensor([0, 9], dtype=torch.int32)
+    out = attention_varlen_triton(q[0].transpose(0, 1), k[0].transpose(0, 1), v[0].transpose(0, 1), cu,
+                                  torch.tensor([0, 12], dtype=torch.int32), 9, 12, causal=True)
+    assert torch.allclose(out.transpose(0, 1), ref[0], atol=1e-5)
+
+
+def test_attention_triton_cpu_lse_is_consistent_with_the_output():
+    """exp(S - lse) are the softmax weights: they reproduce the oracle output and sum to 1 per row."""
+    from fused_attn.triton_fwd import attention_triton
+
+    torch.manual_seed(0)
+    q, k, v = torch.randn(2, 4, 7, 16), torch.randn(2, 2, 11, 16), torch.randn(2, 2, 11, 16)
+    o, lse = attention_triton(q, k, v, causal=True, return_lse=True)
+    assert lse.shape == (2, 4, 7)
+    kk, vv = orc.expand_kv(k, 2), orc.expand_kv(v, 2)
+    s = torch.matmul(q, kk.transpose(-1, -2)) / 4.0
+    s = s.masked_fill(~orc.causal_mask(7, 11), float("-inf"))
+    p = torch.exp(s - lse[..., None])
+    assert torch.allclose(p.sum(-1), torch.ones(2, 4, 7), atol=1e-5)
+    assert torch.allclose(torch.matmul(p, vv), orc.attention(q, k, v, causal=True), atol=1e-5)
