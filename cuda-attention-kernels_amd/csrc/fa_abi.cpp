@@ -38,8 +38,10 @@ size_t dtype_bytes(int32_t dt) {
   }
 }
 
-// Validation shared by every forward entry point.  `fp8_ok` allows FP8 K/V.
-fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok) {
+// Validation shared by every forward entry point.  `fp8_ok` allows FP8 K/V (split-K);
+// `generic_ok` allows fp32 and head dims 16, 32, 256 (prefill and varlen, where the
+// generic kernel takes what the MFMA kernel does not).
+fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok, bool generic_ok) {
   if (p == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params is NULL");
   if (p->batch < 0 || p->heads_q <= 0 || p->heads_kv <= 0 || p->seqlen_q < 0 || p->seqlen_k < 0 ||
       p->head_dim <= 0)
@@ -47,14 +49,17 @@ fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok) {
   if (p->heads_q % p->heads_kv != 0) return fail(FA_ERR_INVALID_ARGUMENT, "H_q must be a multiple of H_kv");
   if (dtype_bytes(p->dtype) == 0 || dtype_bytes(p->kv_dtype) == 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "unknown dtype code");
-  if (p->dtype != FA_DTYPE_F16 && p->dtype != FA_DTYPE_BF16)
-    return fail(FA_ERR_UNSUPPORTED, "q/o dtype must be float16 or bfloat16 for the MFMA kernels");
+  if (p->dtype != FA_DTYPE_F16 && p->dtype != FA_DTYPE_BF16 && !(generic_ok && p->dtype == FA_DTYPE_F32))
+    return fail(FA_ERR_UNSUPPORTED, generic_ok ? "q/o dtype must be float16, bfloat16 or float32"
+                                               : "q/o dtype must be float16 or bfloat16 for split-K");
   if (p->kv_dtype != p->dtype) {
     if (!(fp8_ok && p->kv_dtype == FA_DTYPE_FP8_E4M3))
       return fail(FA_ERR_INVALID_ARGUMENT, "k/v dtype must match q (or be float8_e4m3fn on the split-K path)");
   }
-  if (p->head_dim != 64 && p->head_dim != 128)
-    return fail(FA_ERR_UNSUPPORTED, "head_dim must be 64 or 128 for the MFMA kernels");
+  const int d = p->head_dim;
+  if (generic_ok ? !(d == 16 || d == 32 || d == 64 || d == 128 || d == 256) : !(d == 64 || d == 128))
+    return fail(FA_ERR_UNSUPPORTED, generic_ok ? "head_dim must be 16, 32, 64, 128 or 256"
+                                               : "head_dim must be 64 or 128 on the split-K path");
   if (p->kv_dtype == FA_DTYPE_FP8_E4M3 && (p->k_scale == nullptr || p->v_scale == nullptr))
     return fail(FA_ERR_INVALID_ARGUMENT, "FP8 K/V needs k_scale and v_scale");
   if (!(p->scale == p->scale)) return fail(FA_ERR_INVALID_ARGUMENT, "scale is NaN");
@@ -72,16 +77,17 @@ fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok) {
   if (p->q == nullptr || p->o == nullptr || (!no_keys && (p->k == nullptr || p->v == nullptr)))
     return fail(FA_ERR_INVALID_ARGUMENT, "q, k, v and o must be non-NULL");
   // 16-byte vector loads of Q rows and K/V rows; 8-byte stores of O.
-  const int64_t qvec = 8, kvvec = (int64_t)(16 / dtype_bytes(p->kv_dtype)), ovec = 4;
+  const int64_t qvec = 16 / dtype_bytes(p->dtype), kvvec = (int64_t)(16 / dtype_bytes(p->kv_dtype)),
+                ovec = 8 / dtype_bytes(p->dtype);
   if (!aligned(p->q, 16) || !aligned(p->k, 16) || !aligned(p->v, 16) || !aligned(p->o, 8))
     return fail(FA_ERR_INVALID_ARGUMENT, "q/k/v must be 16-byte aligned and o 8-byte aligned");
   if ((!varlen && (p->q_stride_b % qvec)) || p->q_stride_h % qvec || p->q_stride_n % qvec)
-    return fail(FA_ERR_INVALID_ARGUMENT, "q strides must be multiples of 8 elements (16 bytes)");
+    return fail(FA_ERR_INVALID_ARGUMENT, "q strides must be multiples of 16 bytes");
   if ((!varlen && (p->k_stride_b % kvvec || p->v_stride_b % kvvec)) || p->k_stride_h % kvvec ||
       p->k_stride_n % kvvec || p->v_stride_h % kvvec || p->v_stride_n % kvvec)
     return fail(FA_ERR_INVALID_ARGUMENT, "k/v strides must be multiples of 16 bytes");
   if ((!varlen && (p->o_stride_b % ovec)) || p->o_stride_h % ovec || p->o_stride_n % ovec)
-    return fail(FA_ERR_INVALID_ARGUMENT, "o strides must be multiples of 4 elements (8 bytes)");
+    return fail(FA_ERR_INVALID_ARGUMENT, "o strides must be multiples of 8 bytes");
   // K/V tiles are addressed with 32-bit byte offsets of up to 64 rows from the tile start
   const int64_t kvb = (int64_t)dtype_bytes(p->kv_dtype);
   if (p->k_stride_n < 0 || p->v_stride_n < 0 || p->k_stride_n * kvb >= (1 << 25) || p->v_stride_n * kvb >= (1 << 25))
@@ -95,7 +101,7 @@ extern "C" {
 
 fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream) {
   g_last_error.clear();
-  fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/false);
+  fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/false, /*generic_ok=*/true);
   if (st != FA_OK) return st;
   if (p->lse != nullptr && (p->lse_stride_b < 0 || p->lse_stride_h < 0))
     return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
@@ -107,7 +113,7 @@ fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream) {
 
 fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream) {
   g_last_error.clear();
-  fa_status st = validate(p, /*varlen=*/true, /*fp8_ok=*/false);
+  fa_status st = validate(p, /*varlen=*/true, /*fp8_ok=*/false, /*generic_ok=*/true);
   if (st != FA_OK) return st;
   if (p->lse != nullptr && p->lse_stride_h < 0) return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
   const char* err = nullptr;
@@ -126,7 +132,7 @@ size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_
 fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace, size_t workspace_bytes,
                               void* stream) {
   g_last_error.clear();
-  fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/true);
+  fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/true, /*generic_ok=*/false);
   if (st != FA_OK) return st;
   if (p->lse != nullptr) return fail(FA_ERR_UNSUPPORTED, "LSE output is not available on the split-K path");
   if (split_len <= 0 || split_len % 64 != 0)

@@ -60,6 +60,8 @@ inline fa_status hip_status(hipError_t e, const char** err) {
 
 // Launchers.  They assume fa_abi.cpp has validated `p`.
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
+// fp32, or head dims other than 64 / 128 (fa_generic.hip); run_fwd forwards those here.
+fa_status run_fwd_generic(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
 fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,
                      const char** err);
 

@@ -392,6 +392,8 @@ static hipError_t launch_fwd(const TileArgs& a, hipStream_t stream) {
 }
 
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
+  const bool mfma = (p.dtype == FA_DTYPE_BF16 || p.dtype == FA_DTYPE_F16) && (p.head_dim == 64 || p.head_dim == 128);
+  if (!mfma) return run_fwd_generic(p, varlen, stream, err);
   TileArgs a = common_args(p);
   a.o = p.o;
   a.sob = p.o_stride_b;

@@ -70,8 +70,18 @@ def is_decode_shaped(q: torch.Tensor, k: Optional[torch.Tensor]) -> bool:
     return k is not None and q.shape[-2] <= SPLITK_MAX_Q and k.shape[-2] >= SPLITK_MIN_K
 
 
+SPLITK_DTYPES = (torch.float16, torch.bfloat16)  # the split-K kernel: 16-bit Q with D in {64, 128}
+SPLITK_HEAD_DIMS = (64, 128)
+
+
 def _hip_kernel_for(q: torch.Tensor, k: torch.Tensor) -> str:
-    """Which HIP kernel family serves this call: ``splitk`` or ``fwd``."""
+    """Which HIP kernel family serves this call: ``splitk`` or ``fwd``.
+
+    fp32 and head dims other than 64 / 128 always take ``fwd``, whose generic kernel
+    covers them (the reference's Triton path likewise served every shape).
+    """
+    if q.dtype not in SPLITK_DTYPES or q.shape[-1] not in SPLITK_HEAD_DIMS:
+        return "fwd"
     if os.environ.get("FUSED_ATTN_BACKEND") == "splitk" or is_decode_shaped(q, k):
         return "splitk"
     return "fwd"

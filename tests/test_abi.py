@@ -74,7 +74,8 @@ def _params(**over):
 
 @pytest.mark.parametrize("over,code,msg", [
     (dict(head_dim=96), _hip.FA_ERR_UNSUPPORTED, "head_dim"),
-    (dict(dtype=_hip.F32, kv_dtype=_hip.F32), _hip.FA_ERR_UNSUPPORTED, "dtype"),
+    (dict(head_dim=48), _hip.FA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(dtype=_hip.F32, kv_dtype=_hip.F16), _hip.FA_ERR_INVALID_ARGUMENT, "k/v dtype"),
     (dict(heads_q=3), _hip.FA_ERR_INVALID_ARGUMENT, "multiple"),
     (dict(heads_kv=0), _hip.FA_ERR_INVALID_ARGUMENT, "non-negative"),
     (dict(kv_dtype=_hip.F16), _hip.FA_ERR_INVALID_ARGUMENT, "k/v dtype"),
@@ -140,6 +141,13 @@ def test_splitk_validation(lib):
                                    None) == _hip.FA_ERR_INVALID_ARGUMENT  # fp8 rows need 16-byte strides
     p = _params(lse=0x30000)
     assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need, None) == _hip.FA_ERR_UNSUPPORTED
+    # split-K keeps the MFMA shapes: fp32 and other head dims go to the prefill entry point
+    p = _params(dtype=_hip.F32, kv_dtype=_hip.F32)
+    assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need, None) == _hip.FA_ERR_UNSUPPORTED
+    assert "dtype" in lib.fa_last_error().decode()
+    p = _params(head_dim=32, q_stride_b=4 * 16 * 32, q_stride_h=16 * 32, q_stride_n=32)
+    assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need, None) == _hip.FA_ERR_UNSUPPORTED
+    assert "head_dim" in lib.fa_last_error().decode()
 
 
 def test_make_params_marshals_strides():

@@ -119,8 +119,8 @@ def test_zero_sized_inputs():
     assert torch.all(fused_attn.attention(q, kz, kz, causal=True) == 0)
 
 
-def test_unsupported_dtype_raises_loudly():
-    q = randn(1, 2, 16, 64, dtype=torch.float32)
+def test_unsupported_head_dim_raises_loudly():
+    q = randn(1, 2, 16, 48, dtype=torch.bfloat16)  # fp32 and D in {16, 32, 256} go to the generic kernel
     with pytest.raises(RuntimeError, match="unsupported"):
         _hip.fwd(q, q, q)
 
