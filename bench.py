@@ -144,6 +144,28 @@ def bench_decode(steps, warmup, only_128=False):
     return res
 
 
+def bench_quantize(steps, warmup):
+    """The fused FP8 KV quantiser over one K cache of the FP8 decode workload (bf16 in, e4m3fn + scales out)."""
+    import torch
+
+    import fused_attn
+
+    c = FP8_DECODE
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
+    wall, ev = _time_calls(lambda: fused_attn.quantize_kv_fp8(x), steps, warmup)
+    nblk = -(-c["nk"] // 64)
+    nbytes = x.numel() * 2 + x.numel() + c["b"] * c["hkv"] * nblk * 4
+    return {
+        "workload": f"FP8 KV quantiser B={c['b']} Hkv={c['hkv']} N={c['nk']} D={c['d']}: bf16 -> e4m3fn + fp32 "
+                    "per-64-key scales",
+        "kernel": "quantize_kv_fp8_kernel<bf16,128>",
+        "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+        "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+
 def cpu_baseline():
     """The fp32 oracle on host cores over one (batch, kv-head group) slice of the prefill workload."""
     import torch
@@ -189,6 +211,8 @@ def run_only(which, steps, warmup):
     if which == "prefill":
         flops, wall, ev = bench_prefill(steps, warmup)
         print(f"prefill: {flops / ev / 1e12:.1f} TFLOP/s kernel, {ev * 1e3:.4f} ms", flush=True)
+    elif which == "quantize":
+        print(json.dumps(bench_quantize(steps, warmup)), flush=True)
     elif which in ("decode", "decode128"):
         print(json.dumps(bench_decode(steps, warmup, only_128=which == "decode128")), flush=True)
     else:
@@ -203,7 +227,7 @@ def main():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
-    p.add_argument("--only", choices=["prefill", "decode", "decode128", "copy"], default=None,
+    p.add_argument("--only", choices=["prefill", "decode", "decode128", "quantize", "copy"], default=None,
                    help="run one workload without the JSON line (for profiler runs)")
     a = p.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -244,6 +268,7 @@ def main():
     }
     if not a.no_decode:
         line["decode"] = bench_decode(max(5, a.steps), max(2, a.warmup))
+        line["quantize"] = bench_quantize(max(5, a.steps), max(2, a.warmup))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -174,6 +174,32 @@ int32_t fa_device_supported(int32_t device) {
 
 const char* fa_last_error(void) { return g_last_error.c_str(); }
 
+fa_status fa_quantize_kv_fp8(const fa_quant_params* p, void* stream) {
+  g_last_error.clear();
+  if (p == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params is NULL");
+  if (p->batch < 0 || p->heads < 0 || p->seqlen < 0) return fail(FA_ERR_INVALID_ARGUMENT, "sizes must be non-negative");
+  const int d = p->head_dim;
+  if (!(d == 16 || d == 32 || d == 64 || d == 128 || d == 256))
+    return fail(FA_ERR_UNSUPPORTED, "head_dim must be 16, 32, 64, 128 or 256");
+  if (p->dtype != FA_DTYPE_F32 && p->dtype != FA_DTYPE_F16 && p->dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_UNSUPPORTED, "x must be float32, float16 or bfloat16");
+  if (p->batch == 0 || p->heads == 0 || p->seqlen == 0) return FA_OK;
+  if (p->x == nullptr || p->x8 == nullptr || p->scale == nullptr)
+    return fail(FA_ERR_INVALID_ARGUMENT, "x, x8 and scale must be non-NULL");
+  if (p->x_stride_b < 0 || p->x_stride_h < 0 || p->x_stride_n < 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative stride");
+  // the kernel reads x in 16-byte vectors along head_dim and stores x8 in 8-byte words
+  const int64_t vec = 16 / (int64_t)dtype_bytes(p->dtype);
+  if (p->x_stride_b % vec || p->x_stride_h % vec || p->x_stride_n % vec)
+    return fail(FA_ERR_INVALID_ARGUMENT, "x strides must be multiples of 16 bytes");
+  if (!aligned(p->x, 16) || !aligned(p->x8, 16) || !aligned(p->scale, 4))
+    return fail(FA_ERR_INVALID_ARGUMENT, "x and x8 must be 16-byte aligned, scale 4-byte aligned");
+  const char* err = nullptr;
+  const fa_status st = fa::run_quantize_fp8(*p, reinterpret_cast<hipStream_t>(stream), &err);
+  if (st != FA_OK) return fail(st, err ? err : "launch failed");
+  return FA_OK;
+}
+
 int32_t fa_abi_version(void) { return FA_ABI_VERSION; }
 
 }  // extern "C"

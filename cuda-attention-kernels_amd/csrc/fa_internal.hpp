@@ -37,6 +37,14 @@ struct TileArgs {
   int32_t varlen;
 };
 
+struct QuantArgs {
+  const void* x;
+  uint8_t* x8;
+  float* scale;
+  int64_t sxb, sxh, sxn;
+  int32_t h, n, nblk, total;
+};
+
 struct CombineArgs {
   const float* opart;
   const float* ml;
@@ -62,6 +70,7 @@ inline fa_status hip_status(hipError_t e, const char** err) {
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
 // fp32, or head dims other than 64 / 128 (fa_generic.hip); run_fwd forwards those here.
 fa_status run_fwd_generic(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
+fa_status run_quantize_fp8(const fa_quant_params& p, hipStream_t stream, const char** err);
 fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,
                      const char** err);
 

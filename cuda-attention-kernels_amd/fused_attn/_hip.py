@@ -22,7 +22,7 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libfused_attn_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # fa_dtype codes
 F16, BF16, F32, FP8_E4M3 = 0, 1, 2, 3
@@ -88,6 +88,24 @@ class FwdParams(ctypes.Structure):
     ]
 
 
+class QuantParams(ctypes.Structure):
+    """Mirror of ``fa_quant_params`` (include/fused_attn_hip.h)."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_stride_b", ctypes.c_int64),
+        ("x_stride_h", ctypes.c_int64),
+        ("x_stride_n", ctypes.c_int64),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("seqlen", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("x8", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+    ]
+
+
 _lib = None
 _lib_error: Optional[str] = None
 _lock = threading.Lock()
@@ -110,6 +128,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.fa_attention_splitk.restype = ctypes.c_int
     lib.fa_choose_num_splits.argtypes = [ctypes.c_int32] * 5
     lib.fa_choose_num_splits.restype = ctypes.c_int32
+    lib.fa_quantize_kv_fp8.argtypes = [ctypes.POINTER(QuantParams), ctypes.c_void_p]
+    lib.fa_quantize_kv_fp8.restype = ctypes.c_int
     lib.fa_device_supported.argtypes = [ctypes.c_int32]
     lib.fa_device_supported.restype = ctypes.c_int32
     lib.fa_last_error.argtypes = []
@@ -374,3 +394,31 @@ def choose_num_splits(batch: int, heads: int, seqlen_k: int, seqlen_q: int, num_
 
 def workspace_bytes(batch: int, heads_q: int, seqlen_q: int, head_dim: int, num_splits: int) -> int:
     return int(load_library().fa_splitk_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits))
+
+
+QUANT_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+
+def quantize_kv_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fused FP8 KV quantiser.  x [B,Hkv,N,D] fp32/fp16/bf16 on the GPU -> (float8_e4m3fn
+    [B,Hkv,N,D] contiguous, fp32 scales [B,Hkv,ceil(N/64)]), bit-identical to the reference's
+    torch chain on the GPU (fused_attn/fp8.py:31-45)."""
+    _require_gpu(x)
+    if _FP8 is None:
+        raise RuntimeError("this torch build has no float8_e4m3fn")
+    if x.dim() != 4:
+        raise RuntimeError(f"x must be [B, H, N, D], got {tuple(x.shape)}")
+    lib = load_library()
+    x = _aligned_view(x, 16 // x.element_size(), 16)
+    b, h, n, d = x.shape
+    nblk = -(-n // FP8_QBLOCK)
+    x8 = torch.empty((b, h, n, d), dtype=_FP8, device=x.device)
+    scale = torch.empty((b, h, nblk), dtype=torch.float32, device=x.device)
+    p = QuantParams()
+    p.x, p.x8, p.scale = x.data_ptr(), x8.data_ptr(), scale.data_ptr()
+    p.x_stride_b, p.x_stride_h, p.x_stride_n = _stride(x, 0), _stride(x, 1), _stride(x, 2)
+    p.batch, p.heads, p.seqlen, p.head_dim = b, h, n, d
+    p.dtype = _DTYPE_CODE.get(x.dtype, -1) if x.dtype != _FP8 else -1
+    with torch.cuda.device(x.device):
+        _check(lib.fa_quantize_kv_fp8(ctypes.byref(p), ctypes.c_void_p(_stream(x))), "quantize_kv_fp8")
+    return x8, scale

@@ -8,8 +8,10 @@ block is divided by absmax/448 before the cast (fused_attn/fp8.py:26-45).
     v8, vs = quantize_kv_fp8(v)
     o = attention_fp8(q, k8, ks, v8, vs, causal=True)
 
-The quantiser and dequantiser are torch op chains in the reference's order, so
-their bits equal the reference's on the same torch.  ``attention_fp8`` runs the
+On the GPU the quantiser is one fused HIP kernel (one workgroup per 64-key
+block) whose bytes and scales are bit-identical to the reference's torch chain on
+the GPU; CPU tensors, or ``FUSED_ATTN_BACKEND=reference``, run that torch chain.
+The dequantiser is the reference's torch chain.  ``attention_fp8`` runs the
 HIP split-K kernel, which converts each E4M3 element exactly to q's 16-bit type
 as it stages K/V through LDS, multiplies the score block by
 ``scale * k_scale`` and folds ``v_scale`` into P before the PV product.  Any
@@ -23,6 +25,7 @@ from typing import Optional
 import torch
 
 from . import _hip
+from .ops import _pick_backend
 from .reference import attention_reference
 
 QBLOCK = 64  # keys per scale
@@ -31,8 +34,20 @@ FP8_DTYPE = getattr(torch, "float8_e4m3fn", None)
 
 
 def quantize_kv_fp8(x: torch.Tensor, qblock: int = QBLOCK) -> tuple[torch.Tensor, torch.Tensor]:
-    """x [B, Hkv, N, D] (any float dtype) -> (float8_e4m3fn, same shape; fp32 scales [B, Hkv, ceil(N/qblock)])."""
+    """x [B, Hkv, N, D] (any float dtype) -> (float8_e4m3fn, same shape; fp32 scales [B, Hkv, ceil(N/qblock)]).
+
+    GPU tensors of fp32/fp16/bf16 with D in {16, 32, 64, 128, 256} go to the fused HIP kernel
+    (it raises if the library or device is unusable); other shapes and CPU tensors take the
+    reference's torch chain (fused_attn/fp8.py:31-45)."""
     assert FP8_DTYPE is not None, "this torch build has no float8_e4m3fn"
+    if (x.is_cuda and qblock == QBLOCK and _pick_backend(x) == "hip" and x.dim() == 4
+            and x.dtype in (torch.float32, torch.float16, torch.bfloat16) and x.shape[-1] in _hip.QUANT_HEAD_DIMS):
+        return _hip.quantize_kv_fp8(x)
+    return _quantize_kv_fp8_torch(x, qblock)
+
+
+def _quantize_kv_fp8_torch(x: torch.Tensor, qblock: int = QBLOCK) -> tuple[torch.Tensor, torch.Tensor]:
+    """The reference's torch op chain (fused_attn/fp8.py:31-45), on x's device."""
     b, h, n, d = x.shape
     nblk = -(-n // qblock)
     xf = x.float()

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 /* Element types (reference: DType, csrc/flash_attn.h:7). */
 typedef enum fa_dtype {
@@ -126,6 +126,22 @@ int32_t fa_device_supported(int32_t device);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* fa_last_error(void);
+
+/* FP8 KV-cache quantiser input: x [batch, heads, seqlen, head_dim] in f32/f16/bf16 with element
+   strides (unit head_dim stride); outputs x8 contiguous e4m3fn bytes [batch, heads, seqlen, head_dim]
+   and fp32 scales [batch, heads, ceil(seqlen/64)]. */
+typedef struct fa_quant_params {
+  const void* x;
+  int64_t x_stride_b, x_stride_h, x_stride_n;
+  int32_t batch, heads, seqlen, head_dim;
+  int32_t dtype; /* fa_dtype of x: F16, BF16 or F32 */
+  void* x8;
+  float* scale;
+} fa_quant_params;
+
+/* Per-(batch, head, 64-key block) absmax/448 scaling and e4m3fn rounding, bit-identical to the
+   reference's torch chain quantize_kv_fp8 (fused_attn/fp8.py:31-45).  head_dim in {16, 32, 64, 128, 256}. */
+fa_status fa_quantize_kv_fp8(const fa_quant_params* p, void* stream);
 
 /* FA_ABI_VERSION of the loaded library. */
 int32_t fa_abi_version(void);

@@ -11,7 +11,8 @@ Two independent formulations, so that each pins the other:
   the reference's op order: fused_attn/reference.py:16-95,
   fused_attn/fp8.py:26-56, fused_attn/triton_splitk.py:90-137,153-154;
 * numpy float64 brute force (explicit per-row loops, no matmul library), used
-  on small inputs only.
+  on small inputs only;
+* the FP8 quantiser in numpy float32 with a table-driven e4m3fn encoder.
 
 How each function is pinned (checked in tests/test_oracle.py):
   attention            vs torch.nn.functional.scaled_dot_product_attention
@@ -23,10 +24,15 @@ How each function is pinned (checked in tests/test_oracle.py):
                        in the reference).
   attention_varlen     vs per-sequence dense attention and the brute force,
                        including zero-length sequences.
-  quantize_kv_fp8      vs the reference's round-trip bounds and scale shape
-                       (tests/test_splitk_fp8.py:53-62), vs a closed-form
-                       E4M3 decoder over all 256 codes, and vs a per-block
-                       numpy recomputation of the scales.
+  e4m3fn_encode        vs torch's float8_e4m3fn cast on every code, every
+                       midpoint between neighbouring codes and its fp32
+                       neighbours, subnormals, +-0, NaN and values past 448;
+                       every encoded byte decodes (closed form) to within half
+                       a step of its input.
+  quantize_kv_fp8      vs the reference's torch chain on the CPU bit for bit
+                       (scale_div="true"), vs the reference's round-trip bounds
+                       and scale shape (tests/test_splitk_fp8.py:53-62), and
+                       vs a per-block recomputation of the scales.
   splitk_* / combine   vs unsplit attention (the combine is an exact identity,
                        triton_splitk.py:11-16), for several split lengths.
   choose_num_splits    known answers 27, 1, 2, 1 (tests/test_splitk_fp8.py:44-50).
@@ -181,18 +187,65 @@ def e4m3fn_value(code: int) -> float:
     return -mag if s else mag
 
 
-def quantize_kv_fp8(x: torch.Tensor, qblock: int = QBLOCK):
-    """Per (b, kv-head, qblock keys) amax/448 scale; (x/scale).clamp(+-448) -> e4m3fn (fp8.py:31-45)."""
+_E4M3_POS = None  # magnitudes of the 127 finite non-negative e4m3fn codes 0x00..0x7e, ascending
+
+
+def e4m3fn_encode(x: np.ndarray) -> np.ndarray:
+    """fp32 -> e4m3fn bytes by nearest representable value, ties to the even code; |x| beyond
+    the largest finite value (448) rounds to it up to 464 and is NaN past that
+    (non-saturating, as torch's cast); NaN -> S.1111.111 with x's sign.
+
+    Built from the closed-form decoder ``e4m3fn_value`` (a table lookup, not the bit tricks of
+    a production converter), so it checks torch's cast rather than restating it."""
+    global _E4M3_POS
+    if _E4M3_POS is None:
+        _E4M3_POS = np.array([e4m3fn_value(c) for c in range(0x7f)], dtype=np.float64)
+    xf = np.asarray(x, dtype=np.float32)
+    mag = np.abs(xf).astype(np.float64).ravel()
+    hi = np.clip(np.searchsorted(_E4M3_POS, mag, side="left"), 1, 0x7e)  # table[hi-1] < mag <= table[hi]
+    lo = hi - 1
+    d_lo, d_hi = mag - _E4M3_POS[lo], _E4M3_POS[hi] - mag
+    code = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, hi, np.where(lo % 2 == 0, lo, hi)))
+    code = np.where(mag == 0, 0, code)
+    # above 448 the next step, 480, would be the odd code S.1111.111 (NaN): up to the midpoint
+    # 464 (a tie goes to the even code) the value rounds to 448, past it to NaN
+    code = np.where(mag > 448.0, np.where(mag <= 464.0, 0x7e, 0x7f), code)
+    code = np.where(np.isnan(mag), 0x7f, code).astype(np.uint8)
+    sign = (np.signbit(xf.ravel())).astype(np.uint8) << 7
+    return (code | sign).reshape(xf.shape)
+
+
+def quantize_kv_fp8(x: torch.Tensor, qblock: int = QBLOCK, scale_div: str = "reciprocal"):
+    """Per (b, kv-head, qblock keys) amax/448 scale; (x/scale).clamp(+-448) -> e4m3fn (fp8.py:31-45).
+
+    numpy float32 throughout.  ``scale_div`` is how torch evaluates ``amax / 448.0`` (a tensor
+    divided by a Python scalar, fp8.py:43): on the GPU as a multiply by the float32 reciprocal
+    ("reciprocal"), on the CPU as a true division ("true").  Everything else is the same on
+    both devices: correctly rounded x / scale, NaN-propagating amax and clamps, and the
+    cast rounding to nearest even."""
     b, h, n, d = x.shape
     nblk = -(-n // qblock)
-    xf = x.float()
-    if nblk * qblock != n:
-        xf = torch.cat([xf, xf.new_zeros(b, h, nblk * qblock - n, d)], dim=2)
+    xf = np.zeros((b, h, nblk * qblock, d), dtype=np.float32)
+    xf[:, :, :n] = x.detach().float().cpu().numpy()
     blk = xf.reshape(b, h, nblk, qblock, d)
-    amax = blk.abs().amax(dim=(-1, -2)).clamp_min(1e-12)
-    scale = amax / E4M3_MAX
-    q8 = (blk / scale[..., None, None]).clamp(-E4M3_MAX, E4M3_MAX).to(FP8_DTYPE)
-    return q8.reshape(b, h, nblk * qblock, d)[:, :, :n].contiguous(), scale.contiguous()
+    a = np.abs(blk).reshape(b, h, nblk, -1)
+    amax = np.where(np.isnan(a).any(axis=-1), np.float32(np.nan), np.nanmax(a, axis=-1, initial=0.0))
+    amax = np.where(np.isnan(amax), amax, np.maximum(amax, np.float32(1e-12))).astype(np.float32)
+    if scale_div == "reciprocal":
+        scale = amax * (np.float32(1.0) / np.float32(E4M3_MAX))
+    elif scale_div == "true":
+        scale = amax / np.float32(E4M3_MAX)
+    else:
+        raise ValueError(scale_div)
+    scale = scale.astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        y = (blk / scale[..., None, None]).astype(np.float32)
+    y = np.where(np.isnan(y), y, np.clip(y, -E4M3_MAX, E4M3_MAX)).astype(np.float32)
+    codes = e4m3fn_encode(y).reshape(b, h, nblk * qblock, d)[:, :, :n]
+    x8 = torch.from_numpy(np.ascontiguousarray(codes))
+    if FP8_DTYPE is not None:
+        x8 = x8.view(FP8_DTYPE)
+    return x8, torch.from_numpy(np.ascontiguousarray(scale))
 
 
 def dequantize_kv_fp8(x8: torch.Tensor, scale: torch.Tensor, qblock: int = QBLOCK) -> torch.Tensor:

@@ -42,7 +42,7 @@ def test_struct_layout_matches_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _hip.ABI_VERSION == 1
+    assert lib.fa_abi_version() == _hip.ABI_VERSION == 2
 
 
 def test_choose_num_splits_known_answers(lib):
@@ -178,3 +178,60 @@ def test_aligned_view_copies_only_when_needed():
     assert c is not odd and c.data_ptr() % 16 == 0 and torch.equal(c, odd)
     strided = torch.empty(1, 4, 16, 70, dtype=torch.bfloat16)[..., :64]
     assert _hip._aligned_view(strided, 8, 16).is_contiguous()
+
+
+# ---- fa_quantize_kv_fp8 -----------------------------------------------------------------------
+
+
+def _qparams(**over):
+    p = _hip.QuantParams()
+    # a plausible aligned request; pointers are fake, and every case below is rejected (or empty)
+    # before a launch
+    p.x, p.x8, p.scale = 0x10000, 0x20000, 0x30000
+    p.batch, p.heads, p.seqlen, p.head_dim = 2, 4, 100, 64
+    p.x_stride_b, p.x_stride_h, p.x_stride_n = 4 * 100 * 64, 100 * 64, 64
+    p.dtype = _hip.BF16
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_quant_struct_layout(lib):
+    # pointer, 3 int64 strides, 5 int32 (+4 padding), 2 pointers
+    assert ctypes.sizeof(_hip.QuantParams) == 8 + 3 * 8 + 5 * 4 + 4 + 2 * 8
+    assert _hip.QuantParams.x8.offset == 56
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(head_dim=48), _hip.FA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(head_dim=512), _hip.FA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(dtype=_hip.FP8_E4M3), _hip.FA_ERR_UNSUPPORTED, "float32"),
+    (dict(dtype=7), _hip.FA_ERR_UNSUPPORTED, "float32"),
+    (dict(batch=-1), _hip.FA_ERR_INVALID_ARGUMENT, "non-negative"),
+    (dict(seqlen=-5), _hip.FA_ERR_INVALID_ARGUMENT, "non-negative"),
+    (dict(x=0), _hip.FA_ERR_INVALID_ARGUMENT, "non-NULL"),
+    (dict(scale=0), _hip.FA_ERR_INVALID_ARGUMENT, "non-NULL"),
+    (dict(x_stride_n=-64), _hip.FA_ERR_INVALID_ARGUMENT, "negative"),
+    (dict(x_stride_n=68), _hip.FA_ERR_INVALID_ARGUMENT, "16 bytes"),
+    (dict(x_stride_h=100 * 64 + 4), _hip.FA_ERR_INVALID_ARGUMENT, "16 bytes"),
+    (dict(x=0x10008), _hip.FA_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(x8=0x20008), _hip.FA_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(scale=0x30002), _hip.FA_ERR_INVALID_ARGUMENT, "aligned"),
+])
+def test_quant_validation(lib, over, code, msg):
+    p = _qparams(**over)
+    assert lib.fa_quantize_kv_fp8(ctypes.byref(p), None) == code
+    assert msg in lib.fa_last_error().decode()
+
+
+def test_quant_fp32_rows_need_four_element_strides(lib):
+    # fp32 vectors are 4 elements: a stride of 68 floats is 16-byte aligned, 66 is not
+    assert lib.fa_quantize_kv_fp8(ctypes.byref(_qparams(dtype=_hip.F32, x_stride_n=66)), None) \
+        == _hip.FA_ERR_INVALID_ARGUMENT
+    assert lib.fa_quantize_kv_fp8(None, None) == _hip.FA_ERR_INVALID_ARGUMENT
+
+
+def test_quant_empty_requests_succeed_without_launch(lib):
+    for over in (dict(batch=0), dict(heads=0), dict(seqlen=0), dict(seqlen=0, x=0, x8=0, scale=0)):
+        assert lib.fa_quantize_kv_fp8(ctypes.byref(_qparams(**over)), None) == _hip.FA_OK
+        assert lib.fa_last_error().decode() == ""

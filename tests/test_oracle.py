@@ -127,6 +127,79 @@ def test_fp8_roundtrip_bounds_and_scale_shape():
     assert (kd - k).abs().max() / k.abs().max() < 0.07
 
 
+def _e4m3_probe_values() -> np.ndarray:
+    """Every finite code, every midpoint between neighbouring magnitudes and the fp32 values
+    either side of it, the overflow boundary 464, fp32 subnormals, +-0, +-NaN, and a normal sample."""
+    fin = np.array([v for v in (orc.e4m3fn_value(c) for c in range(256)) if not math.isnan(v)], dtype=np.float32)
+    mag = np.unique(np.abs(fin)).astype(np.float64)
+    mids = ((mag[1:] + mag[:-1]) / 2).astype(np.float32)
+    special = np.array([0.0, 448.0, 449.0, 463.99997, 464.0, 464.00003, 480.0, 1e4, np.inf, 1e-40, 2.0 ** -10,
+                        2.0 ** -10 * 1.0001, 2.0 ** -9 * 1.5, 2.0 ** -9 * 2.5, np.nan], dtype=np.float32)
+    v = np.concatenate([fin, mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf)),
+                        special])
+    v = np.concatenate([v, -v, (np.random.default_rng(0).standard_normal(100000) * 60).astype(np.float32)])
+    return v.astype(np.float32)
+
+
+@pytest.mark.skipif(orc.FP8_DTYPE is None, reason="torch build lacks float8")
+def test_e4m3fn_encoder_matches_torch_cast():
+    v = _e4m3_probe_values()
+    got = orc.e4m3fn_encode(v)
+    want = torch.from_numpy(v).to(orc.FP8_DTYPE).view(torch.uint8).numpy()
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(float(v[i]), int(got[i]), int(want[i])) for i in bad[:8]]
+
+
+def test_e4m3fn_encoder_rounds_to_nearest_even():
+    # closed-form checks that do not go through torch: exact codes map to themselves, a midpoint
+    # goes to the even neighbour, anything else to the nearer one
+    for c in range(256):
+        val = orc.e4m3fn_value(c)
+        if not math.isnan(val):
+            assert orc.e4m3fn_encode(np.float32(val)) == c
+    assert orc.e4m3fn_encode(np.float32(1.0625)) == 0x38  # 1 + 1/16: tie of 1.0 (0x38) and 1.125 (0x39)
+    assert orc.e4m3fn_encode(np.float32(1.1875)) == 0x3a  # tie of 1.125 (0x39) and 1.25 (0x3a)
+    assert orc.e4m3fn_encode(np.float32(2.0 ** -10)) == 0x00  # half the smallest subnormal -> even (zero)
+    assert orc.e4m3fn_encode(np.float32(3 * 2.0 ** -10)) == 0x02  # tie of codes 1 and 2
+    assert orc.e4m3fn_encode(np.float32(464.0)) == 0x7e and orc.e4m3fn_encode(np.float32(465.0)) == 0x7f
+    assert orc.e4m3fn_encode(np.float32(-0.0)) == 0x80 and orc.e4m3fn_encode(np.float32(-np.nan)) == 0xff
+    v = (np.random.default_rng(1).standard_normal(20000) * 50).clip(-448, 448).astype(np.float32)
+    dec = np.array([orc.e4m3fn_value(int(c)) for c in orc.e4m3fn_encode(v)])
+    # within half a step: the step at |x| in [2^e, 2^(e+1)) is 2^(e-3), subnormal step 2^-9
+    step = np.where(np.abs(v) < 2.0 ** -6, 2.0 ** -9, 2.0 ** (np.floor(np.log2(np.abs(v) + 1e-30)) - 3))
+    assert np.all(np.abs(dec - v) <= step / 2 + 1e-12)
+
+
+@pytest.mark.skipif(orc.FP8_DTYPE is None, reason="torch build lacks float8")
+def test_fp8_quantiser_true_division_matches_torch_chain_on_cpu():
+    """scale_div="true" is what the reference's chain gives on the CPU, bit for bit, including
+    blocks that hold NaN, +-inf, zeros and a ragged last block."""
+    torch.manual_seed(3)
+    x = torch.randn(2, 3, 130, 32) * 5
+    x[0, 1, 5, 3] = float("nan")
+    x[1, 2, 100, 0] = float("inf")
+    x[1, 0, 70, 7] = -float("inf")
+    x[0, 0, 64:128] = 0.0
+    x[1, 1, 3] = -0.0
+    nblk = 3
+    xf = torch.cat([x, x.new_zeros(2, 3, nblk * 64 - 130, 32)], dim=2).view(2, 3, nblk, 64, 32)
+    scale = xf.abs().amax(dim=(-1, -2)).clamp_min(1e-12) / 448.0
+    want8 = (xf / scale[..., None, None]).clamp(-448.0, 448.0).to(orc.FP8_DTYPE).view(2, 3, nblk * 64, 32)[:, :, :130]
+    got8, got_s = orc.quantize_kv_fp8(x, scale_div="true")
+    assert torch.equal(got8.view(torch.uint8), want8.contiguous().view(torch.uint8))
+    assert torch.equal(got_s.nan_to_num(nan=-1.0), scale.nan_to_num(nan=-1.0))
+
+
+def test_fp8_quantiser_reciprocal_scale_is_amax_times_float32_reciprocal():
+    torch.manual_seed(4)
+    x = torch.rand(1, 2, 256, 16) * 100
+    _, s = orc.quantize_kv_fp8(x)
+    amax = x.view(1, 2, 4, 64 * 16).abs().amax(-1).numpy().astype(np.float32)
+    assert np.array_equal(s.numpy(), amax * (np.float32(1) / np.float32(448)))
+    _, s_true = orc.quantize_kv_fp8(x, scale_div="true")
+    assert np.array_equal(s_true.numpy(), amax / np.float32(448))
+
+
 @pytest.mark.skipif(orc.FP8_DTYPE is None, reason="torch build lacks float8")
 def test_fp8_scales_equal_blockwise_amax():
     torch.manual_seed(6)
@@ -136,7 +209,7 @@ def test_fp8_scales_equal_blockwise_amax():
     for h in range(2):
         for blk in range(3):
             amax = np.abs(xn[0, h, blk * 64:(blk + 1) * 64]).max()
-            assert s[0, h, blk].item() == pytest.approx(amax / 448.0, rel=1e-7)
+            assert s[0, h, blk].item() == pytest.approx(amax / 448.0, rel=2.5e-7)
     # every quantised magnitude respects the E4M3 range and the block's scale
     x8, s = orc.quantize_kv_fp8(x)
     assert x8.float().abs().max() <= 448.0
