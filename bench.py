@@ -119,10 +119,11 @@ def bench_decode(steps, warmup, only_128=False):
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
             "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
         }
-    del k, v
-    torch.cuda.empty_cache()
     if only_128:
         return res
+    res.update(bench_paged(k, v, steps, warmup, g))
+    del k, v
+    torch.cuda.empty_cache()
     c = FP8_DECODE
     q = torch.randn(c["b"], c["hq"], 1, c["d"], device="cuda", generator=g).bfloat16()
     k8, ks = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
@@ -136,6 +137,32 @@ def bench_decode(steps, warmup, only_128=False):
         res["fp8_decode" + ("" if split else "_default_split")] = {
             "workload": f"FP8-KV split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 n_k={c['nk']} D={c['d']}, "
                         f"e4m3fn + fp32 per-64-key scales, {keys}-key partitions"
+                        f"{'' if split else ' (default partition policy)'}",
+            "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+            "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+        }
+    return res
+
+
+def bench_paged(k, v, steps, warmup, g, page_size=64):
+    """Split-K decode over the same K/V scattered into a shuffled pool of 64-key pages."""
+    import torch
+
+    import fused_attn
+
+    c = DECODE
+    kc, vc, bt, sl = fused_attn.paged_from_dense(k, v, page_size, generator=torch.Generator().manual_seed(0))
+    q = torch.randn(c["b"], c["hq"], 1, c["d"], device="cuda", generator=g).bfloat16()
+    res = {}
+    for split in (128, None):
+        keys = split or fused_attn.ops.default_split_len(1, c["nk"], c["b"], c["hkv"], c["hq"] // c["hkv"])
+        fn = lambda: fused_attn.attention_paged(q, kc, vc, bt, sl, max_seqlen_k=c["nk"], split_len=keys)  # noqa: E731
+        wall, ev = _time_calls(fn, steps, warmup)
+        nbytes = 2 * kc.numel() * 2 + 2 * q.numel() * 2 + bt.numel() * 4
+        res["paged_decode" + ("" if split else "_default_split")] = {
+            "workload": f"paged split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 n_k={c['nk']} D={c['d']} bf16, "
+                        f"{page_size}-key pages in shuffled order, {keys}-key partitions + LSE combine"
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,

@@ -155,6 +155,47 @@ fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* w
   return FA_OK;
 }
 
+fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* kv, int32_t split_len,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (p == nullptr || kv == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params is NULL");
+  fa_fwd_params q = *p;
+  q.k_stride_b = q.v_stride_b = 0;  // keys are found through the block table
+  fa_status st = validate(&q, /*varlen=*/false, /*fp8_ok=*/false, /*generic_ok=*/false);
+  if (st != FA_OK) return st;
+  if (q.lse != nullptr) return fail(FA_ERR_UNSUPPORTED, "LSE output is not available on the split-K path");
+  if (split_len <= 0 || split_len % 64 != 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "split_len must be a positive multiple of 64");
+  if (kv->page_size <= 0 || kv->page_size % 32 != 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "page_size must be a positive multiple of 32");
+  if (kv->num_pages < 0 || kv->block_table_cols < 0) return fail(FA_ERR_INVALID_ARGUMENT, "negative page count");
+  if (q.batch == 0 || q.seqlen_q == 0) return FA_OK;
+  if (kv->block_table == nullptr || kv->seqlens_k == nullptr)
+    return fail(FA_ERR_INVALID_ARGUMENT, "block_table and seqlens_k must be non-NULL");
+  if (!aligned(kv->block_table, 4) || !aligned(kv->seqlens_k, 4))
+    return fail(FA_ERR_INVALID_ARGUMENT, "block_table and seqlens_k must be 4-byte aligned");
+  if (q.batch > 1 && kv->block_table_stride < kv->block_table_cols)
+    return fail(FA_ERR_INVALID_ARGUMENT, "block_table rows overlap (stride below cols)");
+  if ((int64_t)kv->block_table_cols * kv->page_size < q.seqlen_k)
+    return fail(FA_ERR_INVALID_ARGUMENT, "block_table has fewer pages per sequence than seqlen_k needs");
+  const int64_t kvvec = 16 / (int64_t)dtype_bytes(q.kv_dtype);
+  if (kv->k_page_stride < 0 || kv->v_page_stride < 0 || kv->k_page_stride % kvvec || kv->v_page_stride % kvvec)
+    return fail(FA_ERR_INVALID_ARGUMENT, "page strides must be non-negative multiples of 16 bytes");
+  const int32_t splits = q.seqlen_k > 0 ? (q.seqlen_k + split_len - 1) / split_len : 1;
+  const size_t need = fa_splitk_workspace_bytes(q.batch, q.heads_q, q.seqlen_q, q.head_dim, splits);
+  if (workspace == nullptr || workspace_bytes < need) {
+    char buf[160];
+    snprintf(buf, sizeof(buf), "split-K workspace too small: need %zu bytes, got %zu", need,
+             workspace == nullptr ? (size_t)0 : workspace_bytes);
+    return fail(FA_ERR_WORKSPACE, buf);
+  }
+  if (!aligned(workspace, 16)) return fail(FA_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+  const char* err = nullptr;
+  st = fa::run_splitk(q, split_len, workspace, reinterpret_cast<hipStream_t>(stream), &err, kv);
+  if (st != FA_OK) return fail(st, err ? err : "launch failed");
+  return FA_OK;
+}
+
 int32_t fa_choose_num_splits(int32_t batch, int32_t heads, int32_t seqlen_k, int32_t seqlen_q, int32_t num_cus) {
   if (seqlen_q > 64) return 1;  // prefill-sized queries already fill the GPU
   const int64_t programs = (int64_t)batch * heads;

@@ -35,6 +35,12 @@ struct TileArgs {
   float qk_scale; // softmax scale * log2(e)
   int32_t causal;
   int32_t varlen;
+  // paged K/V (split-K decode): k/v are the page pools, skh/skn (svh/svn) strides inside a page
+  const int32_t* block_table;
+  const int32_t* seqlens_k;
+  int64_t sbt;       // block_table row stride
+  int64_t spk, spv;  // page strides of the K and V pools
+  int32_t page_size, num_pages;
 };
 
 struct QuantArgs {
@@ -71,7 +77,8 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
 // fp32, or head dims other than 64 / 128 (fa_generic.hip); run_fwd forwards those here.
 fa_status run_fwd_generic(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
 fa_status run_quantize_fp8(const fa_quant_params& p, hipStream_t stream, const char** err);
+// kv: paged K/V (nullptr for a dense cache)
 fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,
-                     const char** err);
+                     const char** err, const fa_paged_kv* kv = nullptr);
 
 }  // namespace fa

@@ -22,7 +22,7 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libfused_attn_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # fa_dtype codes
 F16, BF16, F32, FP8_E4M3 = 0, 1, 2, 3
@@ -106,6 +106,22 @@ class QuantParams(ctypes.Structure):
     ]
 
 
+class PagedKV(ctypes.Structure):
+    """Mirror of ``fa_paged_kv`` (include/fused_attn_hip.h)."""
+
+    _fields_ = [
+        ("block_table", ctypes.c_void_p),
+        ("block_table_stride", ctypes.c_int64),
+        ("block_table_cols", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("seqlens_k", ctypes.c_void_p),
+        ("num_pages", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("k_page_stride", ctypes.c_int64),
+        ("v_page_stride", ctypes.c_int64),
+    ]
+
+
 _lib = None
 _lib_error: Optional[str] = None
 _lock = threading.Lock()
@@ -128,6 +144,9 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.fa_attention_splitk.restype = ctypes.c_int
     lib.fa_choose_num_splits.argtypes = [ctypes.c_int32] * 5
     lib.fa_choose_num_splits.restype = ctypes.c_int32
+    lib.fa_attention_paged_decode.argtypes = [P, ctypes.POINTER(PagedKV), ctypes.c_int32, ctypes.c_void_p,
+                                              ctypes.c_size_t, ctypes.c_void_p]
+    lib.fa_attention_paged_decode.restype = ctypes.c_int
     lib.fa_quantize_kv_fp8.argtypes = [ctypes.POINTER(QuantParams), ctypes.c_void_p]
     lib.fa_quantize_kv_fp8.restype = ctypes.c_int
     lib.fa_device_supported.argtypes = [ctypes.c_int32]
@@ -385,6 +404,46 @@ def splitk(q, k, v, causal: bool = False, scale: Optional[float] = None, split_l
         _check(lib.fa_attention_splitk(ctypes.byref(p), int(split_len), ctypes.c_void_p(workspace.data_ptr()),
                                        workspace.numel() * workspace.element_size(),
                                        ctypes.c_void_p(_stream(q))), "attention_splitk")
+    return o
+
+
+def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int, causal: bool = False,
+                 scale: Optional[float] = None, split_len: int = 128, workspace: Optional[torch.Tensor] = None):
+    """Split-K decode over a paged cache.  q [B,Hq,Nq,D]; k_cache/v_cache [num_pages, Hkv, page_size, D]
+    (any strides with unit D stride); block_table int32 [B, cols]; seqlens_k int32 [B], both on the GPU."""
+    _require_gpu(q, k_cache, v_cache, block_table, seqlens_k)
+    if block_table.dtype != torch.int32 or seqlens_k.dtype != torch.int32:
+        raise RuntimeError("block_table and seqlens_k must be int32")
+    if block_table.dim() != 2 or seqlens_k.dim() != 1 or block_table.shape[0] != q.shape[0] \
+            or seqlens_k.shape[0] != q.shape[0]:
+        raise RuntimeError("block_table must be [B, pages] and seqlens_k [B] for q's batch B")
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4:
+        raise RuntimeError("k_cache and v_cache must both be [num_pages, Hkv, page_size, D]")
+    lib = load_library()
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    q, k_cache, v_cache = _prep_qkv(q, k_cache, v_cache)
+    bt = block_table if block_table.stride(-1) == 1 else block_table.contiguous()
+    sl = seqlens_k.contiguous()
+    o = _new_output(q)
+    b, hq, nq, d = q.shape
+    max_k = int(max_seqlen_k)
+    splits = -(-max_k // split_len) if max_k > 0 else 1
+    need = lib.fa_splitk_workspace_bytes(b, hq, nq, d, splits)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=q.device)
+    p = make_params(q, k_cache, v_cache, o, causal, scale)
+    p.seqlen_k = max_k
+    p.k_stride_b = p.v_stride_b = 0
+    kv = PagedKV()
+    kv.block_table, kv.block_table_stride, kv.block_table_cols = bt.data_ptr(), bt.stride(0), bt.shape[1]
+    kv.page_size, kv.num_pages = k_cache.shape[2], k_cache.shape[0]
+    kv.seqlens_k = sl.data_ptr()
+    kv.k_page_stride, kv.v_page_stride = _stride(k_cache, 0), _stride(v_cache, 0)
+    with torch.cuda.device(q.device):
+        _check(lib.fa_attention_paged_decode(ctypes.byref(p), ctypes.byref(kv), int(split_len),
+                                             ctypes.c_void_p(workspace.data_ptr()),
+                                             workspace.numel() * workspace.element_size(),
+                                             ctypes.c_void_p(_stream(q))), "attention_paged_decode")
     return o
 
 

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 /* Element types (reference: DType, csrc/flash_attn.h:7). */
 typedef enum fa_dtype {
@@ -91,9 +91,11 @@ typedef struct fa_fwd_params {
   int64_t scale_stride_b, scale_stride_h;
 } fa_fwd_params;
 
-/* Dense FA2 forward on MFMA.  Replaces attention_fwd_mma (csrc/bindings.cpp:63-81),
-   run_attention_fwd_mma (csrc/flash_attn.h:27) and attention_triton
-   (fused_attn/triton_fwd.py:225-265).  Supports f16/bf16, D in {64, 128}. */
+/* Dense FA2 forward.  Replaces attention_fwd_mma (csrc/bindings.cpp:63-81),
+   run_attention_fwd_mma (csrc/flash_attn.h:27), attention_fwd (the SIMT kernel,
+   csrc/flash_attn.cu:222-228) and attention_triton (fused_attn/triton_fwd.py:225-265).
+   f16/bf16 with D in {64, 128} run on MFMA; f32 and D in {16, 32, 256} on the generic
+   fp32-math kernel. */
 fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
 
 /* Packed variable-length forward.  Replaces attention_varlen_triton
@@ -115,6 +117,33 @@ size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_
    num_splits = ceil(seqlen_k / split_len). */
 fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace,
                               size_t workspace_bytes, void* stream);
+
+/* Paged (block-table) K/V for fa_attention_paged_decode.  The K and V pools hold
+   num_pages pages of page_size keys; p->k / p->v point at the pools and
+   p->k_stride_h / k_stride_n (v likewise) are the head and key strides inside a
+   page (p->k_stride_b is unused).  Sequence b's key n lives in page
+   block_table[b * block_table_stride + n / page_size] at offset n % page_size. */
+typedef struct fa_paged_kv {
+  const int32_t* block_table;  /* [batch, block_table_cols] page indices, on the device */
+  int64_t block_table_stride;  /* elements between rows of block_table */
+  int32_t block_table_cols;    /* pages per sequence in the table; cols * page_size >= p->seqlen_k */
+  int32_t page_size;           /* keys per page: a positive multiple of 32 */
+  const int32_t* seqlens_k;    /* [batch] keys per sequence, on the device; values above p->seqlen_k
+                                  are read as p->seqlen_k, negative values as 0 */
+  int32_t num_pages;           /* pages per pool; a table entry outside [0, num_pages) reads as zero keys */
+  int32_t reserved;
+  int64_t k_page_stride, v_page_stride;  /* elements between consecutive pages of each pool */
+} fa_paged_kv;
+
+/* Split-K decode over a paged K/V cache: fa_attention_splitk's kernels (same partials,
+   combine, workspace size and split_len rules) with each sequence's keys gathered
+   through its block table and its own length seqlens_k[b]; p->seqlen_k is the largest
+   length (it sizes the grid) and the causal mask is bottom-right per sequence.
+   f16/bf16, D in {64, 128}.  The reference lists paged K/V for its decode kernels as a
+   roadmap item (README.md:224); the semantics are those of attention_splitk_triton
+   (fused_attn/triton_splitk.py:140-181) applied to each sequence's gathered keys. */
+fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* kv, int32_t split_len,
+                                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Reference split heuristic (fused_attn/triton_splitk.py:130-137):
    min(2*num_cus / (batch*heads), seqlen_k / 256, 64), 1 for seqlen_q > 64. */

@@ -36,6 +36,9 @@ How each function is pinned (checked in tests/test_oracle.py):
   splitk_* / combine   vs unsplit attention (the combine is an exact identity,
                        triton_splitk.py:11-16), for several split lengths.
   choose_num_splits    known answers 27, 1, 2, 1 (tests/test_splitk_fp8.py:44-50).
+  attention_paged      vs dense attention on the K/V that were scattered into randomly
+                       ordered pages (ragged lengths, zero-length sequences, causal), and a
+                       page index outside the pool contributes zero keys.
 """
 from __future__ import annotations
 
@@ -259,6 +262,37 @@ def attention_fp8(q, k8, k_scale, v8, v_scale, causal: bool = False, scale: Opti
     """FP8-KV attention judged against the fp32 oracle on the dequantised K/V (tests/test_splitk_fp8.py:85)."""
     return attention(q.float(), dequantize_kv_fp8(k8, k_scale), dequantize_kv_fp8(v8, v_scale), causal=causal,
                      scale=scale)
+
+
+# ---------------------------------------------------------------------------------------------
+# paged (block-table) K/V: the reference's roadmap item (README.md:224), defined here as dense
+# attention over each sequence's keys gathered through its block table
+# ---------------------------------------------------------------------------------------------
+
+
+def paged_gather(cache: torch.Tensor, block_table: torch.Tensor, seqlen: int, b: int, num_pages=None):
+    """Keys 0..seqlen-1 of sequence b from a [num_pages, H, page_size, D] pool, one key at a time
+    (key n is row n % page_size of page block_table[b, n // page_size]); a page index outside
+    [0, num_pages) contributes zero keys."""
+    num_pages = cache.shape[0] if num_pages is None else num_pages
+    page_size = cache.shape[2]
+    out = cache.new_zeros(cache.shape[1], seqlen, cache.shape[3])
+    bt = block_table.cpu()
+    for n in range(seqlen):
+        pg = int(bt[b, n // page_size])
+        if 0 <= pg < num_pages:
+            out[:, n] = cache[pg, :, n % page_size]
+    return out
+
+
+def attention_paged(q, k_cache, v_cache, block_table, seqlens_k, causal: bool = False, scale: Optional[float] = None):
+    """Per sequence: gather its keys, then the dense oracle with bottom-right causal alignment."""
+    out = torch.zeros(q.shape, dtype=torch.float32)
+    for b, n in enumerate(seqlens_k.cpu().tolist()):
+        k = paged_gather(k_cache.cpu().float(), block_table, n, b)[None]
+        v = paged_gather(v_cache.cpu().float(), block_table, n, b)[None]
+        out[b:b + 1] = attention(q[b:b + 1].cpu().float(), k, v, causal=causal, scale=scale)
+    return out
 
 
 # ---------------------------------------------------------------------------------------------

@@ -186,3 +186,21 @@ def test_attention_triton_cpu_lse_is_consistent_with_the_output():
     p = torch.exp(s - lse[..., None])
     assert torch.allclose(p.sum(-1), torch.ones(2, 4, 7), atol=1e-5)
     assert torch.allclose(torch.matmul(p, vv), orc.attention(q, k, v, causal=True), atol=1e-5)
+
+
+def test_paged_cpu_path_and_pool_builder():
+    """fused_attn.attention_paged on CPU tensors (unfused per-sequence path) vs the oracle, and
+    paged_from_dense's pools gather back to the dense keys."""
+    gen = torch.Generator().manual_seed(5)
+    k = torch.randn(3, 2, 200, 32, generator=gen)
+    v = torch.randn(3, 2, 200, 32, generator=gen)
+    q = torch.randn(3, 8, 2, 32, generator=gen)
+    kc, vc, bt, lens = fused_attn.paged_from_dense(k, v, 64, seqlens=[200, 0, 77], extra_pages=2, generator=gen)
+    assert kc.shape == (3 * 4 + 2, 2, 64, 32) and bt.shape == (3, 4) and bt.dtype == torch.int32
+    from fused_attn.paged import gather_paged
+    assert torch.equal(gather_paged(kc, bt, 200, 0), k[0])
+    assert torch.equal(gather_paged(vc, bt, 77, 2), v[2, :, :77])
+    for causal in (False, True):
+        out = fused_attn.attention_paged(q, kc, vc, bt, lens, causal=causal)
+        ref = orc.attention_paged(q, kc, vc, bt, lens, causal=causal)
+        torch.testing.assert_close(out, ref, atol=1e-5, rtol=1e-5)

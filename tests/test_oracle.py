@@ -254,3 +254,54 @@ def test_split_len_alignment():
     assert orc.split_len_for(1000, 3) == 384 and -(-1000 // 384) == 3
     assert orc.split_len_for(777, 8) == 128 and -(-777 // 128) == 7
     assert orc.split_len_for(2048, 1) == 2048
+
+
+# ---- paged K/V ------------------------------------------------------------------------------------
+
+
+def _scatter_pages(k, page_size, gen):
+    """Dense [B, H, N, D] -> pool [P, H, page_size, D] in a shuffled page order, and its block table."""
+    b, h, n, d = k.shape
+    cols = -(-n // page_size)
+    perm = torch.randperm(b * cols + 3, generator=gen)[:b * cols].view(b, cols)
+    pool = torch.randn(b * cols + 3, h, page_size, d, generator=gen)  # unused pages hold garbage
+    kp = torch.cat([k, k.new_zeros(b, h, cols * page_size - n, d)], dim=2)
+    for bi in range(b):
+        for c in range(cols):
+            pool[perm[bi, c]] = kp[bi, :, c * page_size:(c + 1) * page_size]
+    return pool, perm.to(torch.int32)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_paged_oracle_equals_dense_attention_on_the_scattered_keys(causal):
+    gen = torch.Generator().manual_seed(11)
+    b, hq, hkv, n, d, ps = 4, 4, 2, 150, 16, 32
+    q = torch.randn(b, hq, 3, d, generator=gen)
+    k = torch.randn(b, hkv, n, d, generator=gen)
+    v = torch.randn(b, hkv, n, d, generator=gen)
+    kpool, bt = _scatter_pages(k, ps, gen)
+    vpool = torch.zeros_like(kpool)
+    for bi in range(b):  # V scattered through the same table
+        for c in range(bt.shape[1]):
+            seg = v[bi, :, c * ps:(c + 1) * ps]
+            vpool[bt[bi, c], :, :seg.shape[1]] = seg
+    lens = torch.tensor([150, 0, 33, 64], dtype=torch.int32)
+    got = orc.attention_paged(q, kpool, vpool, bt, lens, causal=causal)
+    for bi, ln in enumerate(lens.tolist()):
+        want = orc.attention(q[bi:bi + 1], k[bi:bi + 1, :, :ln], v[bi:bi + 1, :, :ln], causal=causal)
+        torch.testing.assert_close(got[bi:bi + 1], want, atol=1e-6, rtol=1e-6)
+    assert torch.all(got[1] == 0)  # no keys -> zeros
+
+
+def test_paged_oracle_out_of_pool_pages_read_as_zero_keys():
+    gen = torch.Generator().manual_seed(12)
+    k = torch.randn(1, 1, 96, 8, generator=gen)
+    kpool, bt = _scatter_pages(k, 32, gen)
+    bad = bt.clone()
+    bad[0, 1] = kpool.shape[0] + 7
+    got = orc.paged_gather(kpool, bad, 96, 0)
+    want = k[0].clone()
+    want[:, 32:64] = 0
+    assert torch.equal(got, want)
+    bad[0, 2] = -1
+    assert torch.all(orc.paged_gather(kpool, bad, 96, 0)[:, 64:] == 0)
