@@ -146,25 +146,31 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
     return __builtin_amdgcn_readfirstlane(valid > 0 ? (uint32_t)(valid - 1) * (uint32_t)row_bytes + (uint32_t)(D * 2)
                                                     : 0u);
   };
+  // Tile descriptors (a tile past khi gets a zero-length one: its DMA writes zeros) and
+  // the wave's i-th 1-KiB DMA instruction of a K or V tile.
+  auto k_rsrc = [&](int n0) { return make_rsrc(kbase + (int64_t)n0 * krow_bytes, limit(n0, krow_bytes)); };
+  auto v_rsrc = [&](int n0) { return make_rsrc(vbase + (int64_t)n0 * vrow_bytes, limit(n0, vrow_bytes)); };
+  auto dma_k = [&](const __amdgpu_buffer_rsrc_t& rk, uint16_t* dst, int i) __attribute__((always_inline)) {
+    const int blk = wave * QPW + i;
+    const int byte = blk * 1024 + lane * 16;
+    const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
+    lds_dma16<false>(rk, (uint8_t*)dst + blk * 1024, kperm(r) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16));
+  };
+  auto dma_v = [&](const __amdgpu_buffer_rsrc_t& rv, uint16_t* dst, int i) __attribute__((always_inline)) {
+    const int blk = wave * QPW + i;
+    const int byte = blk * 1024 + lane * 16;
+    const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
+    lds_dma16<false>(rv, (uint8_t*)dst + blk * 1024, r * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16));
+  };
   auto load_k = [&](int n0, uint16_t* dst) {
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)n0 * krow_bytes, limit(n0, krow_bytes));
+    const __amdgpu_buffer_rsrc_t rk = k_rsrc(n0);
 #pragma unroll
-    for (int i = 0; i < QPW; ++i) {
-      const int blk = wave * QPW + i;
-      const int byte = blk * 1024 + lane * 16;
-      const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
-      lds_dma16<false>(rk, (uint8_t*)dst + blk * 1024, kperm(r) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16));
-    }
+    for (int i = 0; i < QPW; ++i) dma_k(rk, dst, i);
   };
   auto load_v = [&](int n0, uint16_t* dst) {
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, limit(n0, vrow_bytes));
+    const __amdgpu_buffer_rsrc_t rv = v_rsrc(n0);
 #pragma unroll
-    for (int i = 0; i < QPW; ++i) {
-      const int blk = wave * QPW + i;
-      const int byte = blk * 1024 + lane * 16;
-      const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
-      lds_dma16<false>(rv, (uint8_t*)dst + blk * 1024, r * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16));
-    }
+    for (int i = 0; i < QPW; ++i) dma_v(rv, dst, i);
   };
 
   // Per-lane LDS element offsets of the MFMA operand reads.
@@ -217,7 +223,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-      for (int r = (kb == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
+      for (int r = (kb == 0 ? 1 : 0); r < 16; ++r) mx = vmax(mx, sc[kb][r]);
     }
     return max_xor32(mx * c);
   };
@@ -225,7 +231,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   // than 2^8; p = 2^(c*s - m_run) then stays <= 256, and O, l stay consistent
   // because both use the same m_run.
   auto update_max = [&](float mt) {
-    const float m_new = fmaxf(m_run, mt);
+    const float m_new = vmax(m_run, mt);
     if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
       const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
       const float alpha = fast_exp2(m_run - m_safe_new);
@@ -239,7 +245,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   // O += V_t P_t from V buffer Vc, then the row max of S_{t+1}.  The max is taken
   // unmasked inside the main block and recomputed only when tile t+1 is masked
   // (or does not exist), so the common path is one basic block.
-  auto body = [&](const uint16_t* Kn, const uint16_t* Vc, f32x16(&cur)[KB], f32x16(&nxt)[KB], int t)
+  // The DMA of the next tiles (K_{t+2} into kd, V_{t+1} into vd: buffers every wave has
+  // finished reading) is issued one instruction every DMA_EVERY slots, under the MFMAs,
+  // instead of as a burst before them (measured: the burst cost ~15% of the loop).
+  auto body = [&](const uint16_t* Kn, const uint16_t* Vc, f32x16(&cur)[KB], f32x16(&nxt)[KB], int t,
+                  const __amdgpu_buffer_rsrc_t& rk, uint16_t* kd, const __amdgpu_buffer_rsrc_t& rv, uint16_t* vd)
       __attribute__((always_inline)) {
     // MFMA slots m = 0 .. NQK-1: S_{t+1} (k-step m / KB, key block m % KB);
     // m = NQK .. NM-1: O += V_t P_t (key block, 16-key half, d block; d fastest).
@@ -251,6 +261,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
     constexpr int EPS = NEXP / NQK;      // micro-steps per S MFMA slot
     constexpr int NMAX = KB * 8;         // max3 steps for S_{t+1}
     static_assert(NEXP % NQK == 0, "exp steps must spread evenly over the S slots");
+    constexpr int NDMA = 2 * QPW, DMA_EVERY = NM / NDMA;
+    static_assert(NM % NDMA == 0, "DMA instructions must spread evenly over the slots");
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) nxt[kb] = f32x16{};
     const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
@@ -284,7 +296,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
     // max step v: scores 2v and 2v+1 of S_{t+1}
     auto max_step = [&](int v) __attribute__((always_inline)) {
       const int kb = v / 8, r = 2 * (v % 8);
-      mx = fmaxf(mx, fmaxf(nxt[kb][r], nxt[kb][r + 1]));
+      mx = vmax(mx, vmax(nxt[kb][r], nxt[kb][r + 1]));
     };
 
 #pragma unroll
@@ -292,6 +304,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       if (m + PD < NM) read(m + PD);
+      if (m % DMA_EVERY == 0) {
+        const int i = m / DMA_EVERY;
+        if (i < QPW) {
+          dma_k(rk, kd, i);
+        } else {
+          dma_v(rv, vd, i - QPW);
+        }
+      }
       const u32x4 op = opnd[m % (PD + 1)];
       if (m < NQK) {
         const int s = m / KB, kb = m % KB;
@@ -316,6 +336,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
       const int n1 = (t + 1) * BN;
       if (t + 1 < n_tiles) {
         if (n1 + BN > mask_from) {
+          // an empty volatile asm cannot be speculated: without it the compiler
+          // if-converts this rare branch and masks every tile in the hot block
+          // (measured: ~150 extra VALU/SALU instructions per tile)
+          __asm__ volatile("");
           mask(nxt, n1);
           mt = tile_max(nxt);
         }
@@ -349,11 +373,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
     uint16_t* k_next = ST == 0 ? k_buf1 : k_buf0;  // holds K_{t+1}
     uint16_t* v_this = ST == 0 ? v_buf0 : v_buf1;  // holds V_t
     uint16_t* v_next = ST == 0 ? v_buf1 : v_buf0;  // takes V_{t+1}
-    if (t + 2 < n_tiles) load_k((t + 2) * BN, k_this);
-    if (t + 1 < n_tiles) load_v((t + 1) * BN, v_next);
     auto& cur = ST == 0 ? s_a : s_b;
     auto& nxt = ST == 0 ? s_b : s_a;
-    body(k_next, v_this, cur, nxt, t);
+    // K_{t+2} and V_{t+1} (zero-length descriptors past the last tile)
+    body(k_next, v_this, cur, nxt, t, k_rsrc((t + 2) * BN), k_this, v_rsrc((t + 1) * BN), v_next);
     lds_dma_wait();
     __syncthreads();
   };

@@ -423,15 +423,15 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
       for (int kb = 0; kb < KB; ++kb) {
         float mx = sacc[kb][0];
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-        mt = fmaxf(mt, mx * sc[kb]);
+        for (int r = 1; r < 16; ++r) mx = vmax(mx, sacc[kb][r]);
+        mt = vmax(mt, mx * sc[kb]);
       }
       mt = max_xor32(mt);
 
       // Lazy rescale: keep the running max unless some row of the wave grew by
       // more than 2^8; p = 2^(c*s - m_run) then stays <= 256 (no overflow risk),
       // and O, l stay consistent because both use the same m_run.
-      const float m_new = fmaxf(m_run, mt);
+      const float m_new = vmax(m_run, mt);
       if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
         const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
         const float alpha = fast_exp2(m_run - m_safe_new);
