@@ -126,7 +126,8 @@ size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_
                                  int32_t num_splits) {
   if (batch <= 0 || heads_q <= 0 || seqlen_q <= 0 || head_dim <= 0 || num_splits <= 0) return 0;
   const size_t rows = (size_t)batch * (size_t)heads_q * (size_t)seqlen_q * (size_t)num_splits;
-  return rows * ((size_t)head_dim + 2) * sizeof(float);
+  // 16-bit normalised partial outputs, then fp32 (max, sum) pairs
+  return rows * ((size_t)head_dim * 2 + 2 * sizeof(float));
 }
 
 fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace, size_t workspace_bytes,

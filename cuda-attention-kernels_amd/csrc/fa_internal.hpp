@@ -52,7 +52,7 @@ struct QuantArgs {
 };
 
 struct CombineArgs {
-  const float* opart;
+  const uint16_t* opart;  // normalised partials in the output's 16-bit type
   const float* ml;
   void* o;
   int64_t sob, soh, son;

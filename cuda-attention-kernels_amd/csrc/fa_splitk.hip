@@ -2,8 +2,12 @@
 //
 //   * attn_splitk_kernel: the reference's _attn_splitk_kernel
 //     (fused_attn/triton_splitk.py:29-96), including the FP8 K/V variant of
-//     _attn_fp8_kernel (fused_attn/fp8.py:59-122): un-normalised fp32 partial
-//     outputs plus (max, sum) statistics in the log2 domain, one per key partition;
+//     _attn_fp8_kernel (fused_attn/fp8.py:59-122): one partial output per key
+//     partition plus its (max, sum) statistics in the log2 domain.  The reference
+//     keeps un-normalised fp32 partials; here a partial is normalised by its own sum
+//     (a convex combination of V rows) and stored in Q's 16-bit type, which halves
+//     the partial traffic (a 128-key partition writes and re-reads D * 2 bytes per
+//     row instead of D * 4) at the cost of one 16-bit rounding;
 //   * splitk_combine_kernel: the log-sum-exp merge of the partitions
 //     (_splitk_combine_kernel, fused_attn/triton_splitk.py:99-127).
 //
@@ -312,20 +316,22 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   }
   const int qlim = qi + offset;  // last key this lane's row may see (causal)
 
-  // Un-normalised partial + log2-domain statistics of partition `part`
-  // (triton_splitk.py:90-96), then the state restarts for the next partition.
+  // Partial of partition `part`, normalised by its row sum and rounded to E, plus its
+  // log2-domain statistics (triton_splitk.py:90-96); then the state restarts for the
+  // next partition.  A partition with no visible key (l = 0) stores zeros.
   auto emit_partial = [&](int part) __attribute__((always_inline)) {
     const float l_tot = sum_xor32(l_run);  // each lane summed its 16 of the row's keys per tile
     if (wave_active && row_ok) {
       const int64_t prow = ((int64_t)(b * a.hq + hq) * seq_q + qi) * a.n_split + part;
-      float* op = (float*)a.o + prow * D;
+      uint16_t* op = (uint16_t*)a.o + prow * D;
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
           const int d0 = d * 32 + 8 * rq + 4 * g;
-          st16(op + d0, __builtin_bit_cast(u32x4, f32x4{oacc[d][4 * rq], oacc[d][4 * rq + 1], oacc[d][4 * rq + 2],
-                                                        oacc[d][4 * rq + 3]}));
+          st8(op + d0, u32x2{pack2<E>(oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv),
+                             pack2<E>(oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv)});
         }
       }
       if (g == 0) st8(a.ml + prow * 2, __builtin_bit_cast(u32x2, f32x2{m_run, l_tot}));
@@ -500,10 +506,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   for (int part = part0 + (n_tiles + tiles_per_part - 1) / tiles_per_part; part < part_end; ++part) emit_partial(part);
 }
 
-// Log-sum-exp merge of split-K partials (triton_splitk.py:99-127):
-//   m = max_s m_s;  w_s = 2^(m_s - m);  O = sum_s w_s O_s / sum_s w_s l_s   (0 when the sum is 0)
+// Log-sum-exp merge of split-K partials (triton_splitk.py:99-127), with each partial
+// O_s stored normalised (O_s = un-normalised partial / l_s):
+//   m = max_s m_s;  w_s = 2^(m_s - m) l_s;  O = sum_s w_s O_s / sum_s w_s   (0 when the sum is 0)
 // One 256-thread workgroup per output row; D/4 threads cover a partial row with
-// float4 loads, so 256/(D/4) splits are read concurrently.
+// 8-byte loads (4 elements), so 256/(D/4) splits are read concurrently.
 template <int D, class E>
 __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c) {
   constexpr int TPS = D / 4;
@@ -516,7 +523,7 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
   const int64_t row = blockIdx.x;  // (b, hq, qi) flattened
   const int S = c.n_split;
   const float* ml = c.ml + row * S * 2;
-  const float* op = c.opart + row * (int64_t)S * D;
+  const uint16_t* op = c.opart + row * (int64_t)S * D;
   const int tid = (int)threadIdx.x;
 
   float m = NEG_INF;
@@ -537,9 +544,10 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
 #pragma unroll 4
   for (int s = sg; s < S; s += SPB) {
     const f32x2 st = __builtin_bit_cast(f32x2, ld8(ml + 2 * s));
-    const float w = fast_exp2(st[0] - m_safe);
-    l += w * st[1];
-    acc += w * __builtin_bit_cast(f32x4, ld16(op + (int64_t)s * D + 4 * dq));
+    const float w = fast_exp2(st[0] - m_safe) * st[1];
+    l += w;
+    const u32x2 pv = ld8(op + (int64_t)s * D + 4 * dq);
+    acc += w * f32x4{lo_f32<E>(pv[0]), hi_f32<E>(pv[0]), lo_f32<E>(pv[1]), hi_f32<E>(pv[1])};
   }
   part[sg][dq] = acc;
   if (dq == 0) lpart[sg] = l;
@@ -675,8 +683,8 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
     return FA_ERR_UNSUPPORTED;
   }
   a.total = (int32_t)total;
-  a.o = workspace;
-  a.ml = (float*)workspace + out_rows * S * p.head_dim;
+  a.o = workspace;  // 16-bit partials [rows, S, D], then (m, l) pairs [rows, S, 2]
+  a.ml = (float*)((uint8_t*)workspace + out_rows * S * p.head_dim * 2);
   const bool fp8 = p.kv_dtype == FA_DTYPE_FP8_E4M3;
   const bool bf = p.dtype == FA_DTYPE_BF16;
   hipError_t e = hipErrorInvalidValue;
@@ -689,7 +697,7 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
   if (e != hipSuccess) return hip_status(e, err);
 
   CombineArgs c{};
-  c.opart = (const float*)a.o;
+  c.opart = (const uint16_t*)a.o;
   c.ml = a.ml;
   c.o = p.o;
   c.sob = p.o_stride_b;

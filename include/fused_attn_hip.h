@@ -103,8 +103,9 @@ fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
 fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream);
 
 /* Bytes of workspace fa_attention_splitk needs for `num_splits` key partitions:
-   fp32 partial outputs [B, Hq, Nq, S, D] plus (max, sum) pairs [B, Hq, Nq, S, 2]
-   (reference partial buffers: fused_attn/triton_splitk.py:156-158). */
+   partial outputs [B, Hq, Nq, S, D] in q's 16-bit type, each normalised by its own
+   row sum, plus fp32 (max, sum) pairs [B, Hq, Nq, S, 2] (the reference keeps fp32
+   un-normalised partials: fused_attn/triton_splitk.py:156-158). */
 size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q, int32_t head_dim,
                                  int32_t num_splits);
 

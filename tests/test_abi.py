@@ -53,7 +53,8 @@ def test_choose_num_splits_known_answers(lib):
 
 
 def test_workspace_bytes(lib):
-    assert lib.fa_splitk_workspace_bytes(32, 32, 1, 128, 256) == 32 * 32 * 256 * 130 * 4
+    # 16-bit partials plus fp32 (max, sum) pairs per (row, partition)
+    assert lib.fa_splitk_workspace_bytes(32, 32, 1, 128, 256) == 32 * 32 * 256 * (128 * 2 + 8)
     assert lib.fa_splitk_workspace_bytes(0, 32, 1, 128, 256) == 0
 
 
