@@ -123,8 +123,15 @@ __device__ __forceinline__ float sum2<F16>(uint32_t w, float acc) {
 
 // Raw buffer resource over [base, base + num_bytes): loads at offsets >= num_bytes
 // return zeros (hardware range check), which zero-fills tails without branches.
+// Callers pass wave-uniform values; the readfirstlanes state that to the compiler, so
+// the descriptor always lives in SGPRs (a descriptor it cannot prove uniform is used
+// through a per-lane "waterfall" loop around every load: measured 16x slower).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, 0x00020000);
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)addr);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(lo | (hi << 32)), (short)0,
+                                           (int)__builtin_amdgcn_readfirstlane(num_bytes), 0x00020000);
 }
 // 16-byte buffer load; STREAM sets the non-temporal hint for data read exactly once.
 template <bool STREAM>
