@@ -47,12 +47,25 @@ def attn_flops(b, h, n, d, causal):
     return f / 2 if causal else f
 
 
+WARMUP_MIN_S = 0.2  # untimed warm-up per workload: at least this long, and at least `warmup` calls
+
+
 def _time_calls(fn, steps, warmup):
-    """Wall time per call (synchronised both sides) and mean per-launch duration from HIP events."""
+    """Wall time per call (synchronised both sides) and mean per-launch duration from HIP events.
+
+    Before the timed region the workload runs untimed for ``warmup`` calls and at least
+    WARMUP_MIN_S seconds (the reference's benchmark warms up by time too: triton's do_bench,
+    benchmarks/bench.py:49-53).  MI355X clocks take some tens of milliseconds of load to
+    settle; a cold first workload measured ~15% slow after 5 calls."""
     import torch
 
-    for _ in range(warmup):
+    t_end = time.perf_counter() + WARMUP_MIN_S
+    done = 0
+    while done < warmup or time.perf_counter() < t_end:
         fn()
+        done += 1
+        if done % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -91,6 +104,50 @@ def bench_prefill(steps, warmup):
     wall, ev = _time_calls(lambda: fused_attn.attention(q, k, v, causal=True), steps, warmup)
     flops = attn_flops(c["b"], c["hq"], c["n"], c["d"], True)
     return flops, wall, ev
+
+
+def bench_prefill_extras(steps, warmup):
+    """The other prefill configurations: D=64 MHA, the [B,N,H,D] view, and the 16-sequence varlen batch."""
+    import torch
+
+    import fused_attn
+
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(0)
+
+    def entry(name, workload, fn, flops):
+        out = fn()
+        assert not torch.isnan(out).any()
+        wall, ev = _time_calls(fn, steps, warmup)
+        res[name] = {"workload": workload, "ms": round(wall * 1e3, 4), "TFLOP_s": round(flops / wall / 1e12, 1),
+                     "TFLOP_s_events": round(flops / ev / 1e12, 1),
+                     "mfma_frac": round(flops / ev / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+    q = torch.randn(4, 16, 4096, 64, device="cuda", generator=g).bfloat16()
+    k = torch.randn(4, 16, 4096, 64, device="cuda", generator=g).bfloat16()
+    v = torch.randn(4, 16, 4096, 64, device="cuda", generator=g).bfloat16()
+    entry("prefill_d64_mha", "causal MHA prefill B=4 Hq=Hkv=16 N=4096 D=64 bf16",
+          lambda: fused_attn.attention(q, k, v, causal=True), attn_flops(4, 16, 4096, 64, True))
+    c = PREFILL
+    q = torch.randn(c["b"], c["n"], c["hq"], c["d"], device="cuda", generator=g).bfloat16().transpose(1, 2)
+    k = torch.randn(c["b"], c["n"], c["hkv"], c["d"], device="cuda", generator=g).bfloat16().transpose(1, 2)
+    v = torch.randn(c["b"], c["n"], c["hkv"], c["d"], device="cuda", generator=g).bfloat16().transpose(1, 2)
+    entry("prefill_bnhd_view", f"causal GQA prefill B={c['b']} Hq={c['hq']} Hkv={c['hkv']} N={c['n']} D={c['d']} bf16, "
+          "[B,N,H,D] storage viewed as [B,H,N,D]",
+          lambda: fused_attn.attention(q, k, v, causal=True), attn_flops(c["b"], c["hq"], c["n"], c["d"], True))
+    lens = torch.randint(0, 4097, (16,), generator=torch.Generator().manual_seed(0)).tolist()
+    lens[0], lens[1] = 0, 1
+    total = sum(lens)
+    q = torch.randn(total, 32, 128, device="cuda", generator=g).bfloat16()
+    k = torch.randn(total, 8, 128, device="cuda", generator=g).bfloat16()
+    v = torch.randn(total, 8, 128, device="cuda", generator=g).bfloat16()
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+    mx = max(lens)
+    entry("varlen_prefill", f"varlen causal prefill, 16 sequences (lengths U[0,4096] by seed 0, one 0, one 1; "
+          f"{total} tokens) Hq=32 Hkv=8 D=128 bf16",
+          lambda: fused_attn.attention_varlen(q, k, v, cu, cu, mx, mx, causal=True),
+          sum(attn_flops(1, 32, n, 128, True) for n in lens))
+    return res
 
 
 def bench_decode(steps, warmup, only_128=False):
@@ -279,6 +336,7 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "warmup_min_s_per_workload": WARMUP_MIN_S,
         "ms_per_step": round(wall * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -293,6 +351,7 @@ def main():
                      "traffic": _traffic_bytes(), "kernel": "attn_fwd_kernel<128,BF16>",
                      "kernel_ms": round(ev * 1e3, 4)},
     }
+    line["prefill_other"] = bench_prefill_extras(max(5, a.steps // 2), max(2, a.warmup))
     if not a.no_decode:
         line["decode"] = bench_decode(max(5, a.steps), max(2, a.warmup))
         line["quantize"] = bench_quantize(max(5, a.steps), max(2, a.warmup))
