@@ -63,16 +63,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   // through one or two units at a time and re-reads K/V from its L2.  Inside a unit
   // the query blocks go by rank, heaviest causal blocks first, all heads of the unit
   // at each rank, which keeps the XCD's CUs evenly loaded to the end.
+  //
+  // Varlen batches are the exception: their sequences differ in length, and ranges of
+  // whole sequences per XCD load the XCDs unevenly (measured: a 16-sequence batch ran at
+  // 0.18 of peak).  There the blocks go rank-major over all (sequence, q-head) pairs in
+  // launch order, heaviest ranks first, and the dispatcher spreads them over the XCDs.
   constexpr int64_t kL2UnitBytes = int64_t{4} << 20;
-  const int logical = xcd_remap((int)blockIdx.x, a.total);
   const int nbh = a.total / a.n_rowblk;  // (batch, q-head) pairs
-  const int64_t kv_head_bytes = (int64_t)max(a.nk, 1) * D * 2 * 2;
-  const int unit_heads = max(1, (int)(kL2UnitBytes / kv_head_bytes)) * a.group;
-  const int unit = logical / (unit_heads * a.n_rowblk);
-  const int within = logical % (unit_heads * a.n_rowblk);
-  const int unit_size = min(unit_heads, nbh - unit * unit_heads);
-  const int mrev = within / unit_size;
-  int item = unit * unit_heads + within % unit_size;
+  int mrev, item;
+  if (a.varlen) {
+    mrev = (int)blockIdx.x / nbh;
+    item = (int)blockIdx.x % nbh;
+  } else {
+    const int logical = xcd_remap((int)blockIdx.x, a.total);
+    const int64_t kv_head_bytes = (int64_t)max(a.nk, 1) * D * 2 * 2;
+    const int unit_heads = max(1, (int)(kL2UnitBytes / kv_head_bytes)) * a.group;
+    const int unit = logical / (unit_heads * a.n_rowblk);
+    const int within = logical % (unit_heads * a.n_rowblk);
+    const int unit_size = min(unit_heads, nbh - unit * unit_heads);
+    mrev = within / unit_size;
+    item = unit * unit_heads + within % unit_size;
+  }
   const int gi = item % a.group;
   item /= a.group;
   const int kvh = item % a.hkv;
