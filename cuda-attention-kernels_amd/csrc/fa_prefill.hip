@@ -2,7 +2,7 @@
 //
 // Serves the reference's dense and varlen prefill, attn_fwd_mma_kernel
 // (csrc/flash_attn_mma.cu:63-242) and _attn_fwd_kernel
-// (fused_attn/triton_fwd.py:85-172), for 16-bit Q/K/V with D in {64, 128}.
+// (fused_attn/triton_fwd.py:85-172), for 16-bit Q/K/V with D in {64, 128, 256}.
 //
 // A workgroup of 4 waves covers 128 queries of one q-head; wave w owns 32 of
 // them.  K and V stream through LDS in 64-key tiles (128 at D=64), each in two buffers filled
@@ -37,17 +37,20 @@
 namespace fa {
 
 template <int D, class E>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attn_fwd_kernel(const TileArgs a) {
-  // 64-key tiles at D=128, 128-key tiles at D=64: 16 KiB per K (or V) tile and 32 MFMAs per
-  // iteration either way (measured: D=64 prefill 3% faster than with 64-key tiles)
-  constexpr int NW = 4, BN = D == 64 ? 128 : 64;
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
+attn_fwd_kernel(const TileArgs a) {
+  // 64-key tiles at D=128, 128-key tiles at D=64, 32-key tiles at D=256: 16 KiB per K (or V)
+  // tile and 32 MFMAs per iteration in every case (measured: D=64 prefill 3% faster than with
+  // 64-key tiles).  At D=256 the fp32 output accumulator alone takes 128 registers per lane,
+  // so the kernel runs one wave per SIMD there.
+  constexpr int NW = 4, BN = D == 64 ? 128 : (D == 256 ? 32 : 64);
   using Shape = TileShape<D, BN>;
   constexpr int TILE = Shape::TILE;
   constexpr int KB = BN / 32;  // 32-key MFMA blocks per tile
   constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
   constexpr int DB = D / 32;   // 32-wide d blocks of O^T
   constexpr int QPW = (TILE * 2 / 1024) / NW;  // 1-KiB DMA blocks per wave per K (or V) tile
-  static_assert(D == 64 || D == 128, "head dim");
+  static_assert(D == 64 || D == 128 || D == 256, "head dim");
   static_assert((TILE * 2) % (1024 * NW) == 0, "direct loads must split evenly over the waves");
   constexpr float NEG_INF = -__builtin_inff();
 
@@ -271,9 +274,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
     // sched_barrier after every slot keeps this order through scheduling.
     constexpr int NQK = KS * KB, NPV = KB * 2 * DB, NM = NQK + NPV, PD = 3;
     constexpr int NEXP = KB * 8;         // exp micro-steps (2 scores each) for S_t
-    constexpr int EPS = NEXP / NQK;      // micro-steps per S MFMA slot
     constexpr int NMAX = KB * 8;         // max3 steps for S_{t+1}
-    static_assert(NEXP % NQK == 0, "exp steps must spread evenly over the S slots");
+    // exp step u runs in S slot u * NQK / NEXP: several per slot, or one every few slots
+    static_assert(NEXP % NQK == 0 || NQK % NEXP == 0, "exp steps must spread evenly over the S slots");
     constexpr int NDMA = 2 * QPW, DMA_EVERY = NM / NDMA;
     static_assert(NM % NDMA == 0, "DMA instructions must spread evenly over the slots");
 #pragma unroll
@@ -330,7 +333,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
         const int s = m / KB, kb = m % KB;
         nxt[kb] = mfma32<E>(op, qf[s], nxt[kb]);
 #pragma unroll
-        for (int q = 0; q < EPS; ++q) exp_step(m * EPS + q);
+        for (int u = 0; u < NEXP; ++u) {
+          if (u * NQK / NEXP == m) exp_step(u);
+        }
       } else {
         const int i = m - NQK, kb = i / (2 * DB), h = (i / DB) % 2, d = i % DB;
         oacc[d] = mfma32<E>(op, pf[kb][h], oacc[d]);
@@ -428,7 +433,8 @@ static hipError_t launch_fwd(const TileArgs& a, hipStream_t stream) {
 }
 
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
-  const bool mfma = (p.dtype == FA_DTYPE_BF16 || p.dtype == FA_DTYPE_F16) && (p.head_dim == 64 || p.head_dim == 128);
+  const bool mfma = (p.dtype == FA_DTYPE_BF16 || p.dtype == FA_DTYPE_F16) &&
+                    (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256);
   if (!mfma) return run_fwd_generic(p, varlen, stream, err);
   TileArgs a = common_args(p);
   a.o = p.o;
@@ -462,6 +468,8 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
     e = bf ? launch_fwd<128, BF16>(a, stream) : launch_fwd<128, F16>(a, stream);
   } else if (p.head_dim == 64) {
     e = bf ? launch_fwd<64, BF16>(a, stream) : launch_fwd<64, F16>(a, stream);
+  } else if (p.head_dim == 256) {
+    e = bf ? launch_fwd<256, BF16>(a, stream) : launch_fwd<256, F16>(a, stream);
   }
   return hip_status(e, err);
 }

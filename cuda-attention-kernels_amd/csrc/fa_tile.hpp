@@ -9,18 +9,23 @@ namespace fa {
 // are XOR-swizzled per row so that every read pattern hits all 64 LDS banks once,
 // and so that direct global->LDS loads (which write 64 lanes x 16 B contiguously)
 // can fill a tile.  Physical chunk = logical chunk ^ swizzle(row).
+//
+// A chunk's bank group (16 bytes = 4 of the 64 banks) is its physical index mod 16,
+// since rows are multiples of 256 bytes at D >= 128.  At D = 256 a row is two bank
+// lines; the XOR values stay below 16, so they keep a chunk's high bit and give the
+// same bank pattern as at D = 128.
 template <int D, int BN>
 struct TileShape {
-  static constexpr int CPR = D / 8;             // 16-byte chunks per row
-  static constexpr int ROWS_PER_256B = 128 / D;  // rows sharing one 256-byte bank line
-  static constexpr int TILE = BN * D;            // elements per K (or V) tile
-  static constexpr int STAGE = 2 * TILE;         // K then V
+  static constexpr int CPR = D / 8;                         // 16-byte chunks per row
+  static constexpr int ROWS_PER_256B = D >= 128 ? 1 : 128 / D;  // rows sharing one 256-byte bank line
+  static constexpr int TILE = BN * D;                       // elements per K (or V) tile
+  static constexpr int STAGE = 2 * TILE;                    // K then V
   // K rows are read 16 at a time at one logical chunk: map them to 16 distinct bank groups.
-  __device__ static constexpr int swz_k(int row) { return (row / ROWS_PER_256B) % CPR; }
+  __device__ static constexpr int swz_k(int row) { return (row / ROWS_PER_256B) % (CPR < 16 ? CPR : 16); }
   // V is read transposed: 4 consecutive rows (starting at a multiple of 4) x 4 chunks
   // (starting at a multiple of 4) per 32 lanes.
   __device__ static constexpr int swz_v(int row) {
-    return D == 128 ? 4 * (row & 3) + ((row >> 2) & 3) : 4 * ((row >> 1) & 1);
+    return D >= 128 ? 4 * (row & 3) + ((row >> 2) & 3) : 4 * ((row >> 1) & 1);
   }
 };
 

@@ -39,8 +39,6 @@ _STATUS_NAME = {
     FA_ERR_HIP: "HIP error",
 }
 
-HEAD_DIMS = (64, 128)
-DTYPES = (torch.float16, torch.bfloat16)
 FP8_QBLOCK = 64  # keys per FP8 scale block; split-K partitions are multiples of it
 
 
@@ -316,12 +314,6 @@ def _require_gpu(*ts: torch.Tensor) -> None:
         raise RuntimeError(
             f"fused_attn HIP backend unavailable on {dev}: "
             + (_lib_error or "device is not a gfx950 GPU (set FUSED_ATTN_BACKEND=reference to run the unfused path)"))
-
-
-def supports(q: torch.Tensor, k: torch.Tensor) -> bool:
-    """Shapes/dtypes the MFMA kernels implement (the mma kernel's checks, csrc/bindings.cpp:39-43)."""
-    return (q.dtype in DTYPES and k.dtype in (q.dtype, _FP8) and q.shape[-1] in HEAD_DIMS
-            and q.shape[-1] == k.shape[-1])
 
 
 # ----------------------------------------------------------------------------------------------

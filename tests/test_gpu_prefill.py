@@ -28,7 +28,7 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k", SHAPES)
 def test_prefill_matches_oracle(b, h_q, h_kv, n_q, n_k, causal, head_dim, dtype):
@@ -83,16 +83,17 @@ def test_unaligned_views_are_copied_not_misread():
     assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu())) <= TOL[torch.bfloat16]
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("causal", [False, True])
-def test_lse_output(causal):
-    announce(f"lse causal={causal}")
+def test_lse_output(causal, d):
+    announce(f"lse causal={causal} d={d}")
     torch.manual_seed(0)
-    q = randn(2, 8, 100, 128, dtype=torch.bfloat16)
-    k = randn(2, 2, 77, 128, dtype=torch.bfloat16)
-    v = randn(2, 2, 77, 128, dtype=torch.bfloat16)
+    q = randn(2, 8, 100, d, dtype=torch.bfloat16)
+    k = randn(2, 2, 77, d, dtype=torch.bfloat16)
+    v = randn(2, 2, 77, d, dtype=torch.bfloat16)
     out, lse = _hip.fwd(q, k, v, causal=causal, return_lse=True)
     qf, kf = q.float().cpu(), orc.expand_kv(k.float().cpu(), 4)
-    s = torch.matmul(qf, kf.transpose(-1, -2)) / math.sqrt(128)
+    s = torch.matmul(qf, kf.transpose(-1, -2)) / math.sqrt(d)
     if causal:
         s = s.masked_fill(~orc.causal_mask(100, 77), float("-inf"))
     ref = torch.logsumexp(s, dim=-1)
@@ -120,7 +121,7 @@ def test_zero_sized_inputs():
 
 
 def test_unsupported_head_dim_raises_loudly():
-    q = randn(1, 2, 16, 48, dtype=torch.bfloat16)  # fp32 and D in {16, 32, 256} go to the generic kernel
+    q = randn(1, 2, 16, 48, dtype=torch.bfloat16)  # fp32 and D in {16, 32} go to the generic kernel
     with pytest.raises(RuntimeError, match="unsupported"):
         _hip.fwd(q, q, q)
 
@@ -151,3 +152,28 @@ def test_baseline_prefill_configs(cfg):
     err = max_err(out, ref)
     print(f"max_abs_err={err:.3e}", flush=True)
     assert err <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_head_dim_256_views_varlen_and_decode_shapes(dtype):
+    """D=256 on the MFMA kernel (32-key tiles, one wave per SIMD): the [B,N,H,D] view, a
+    varlen batch with an empty sequence, and a decode-shaped call (split-K takes D<=128)."""
+    announce(f"d=256 extra shapes {dtype}")
+    torch.manual_seed(0)
+    x = randn(2, 150, 3, 4, 256, dtype=dtype)
+    q, k, v = (x[:, :, i].transpose(1, 2) for i in range(3))
+    out = fused_attn.attention(q, k, v, causal=True)
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=True)) <= TOL[dtype]
+    lens = [37, 0, 300, 1]
+    qv, cu, mx = fused_attn.pack_varlen([randn(n, 8, 256, dtype=dtype) for n in lens])
+    kv, _, _ = fused_attn.pack_varlen([randn(n, 2, 256, dtype=dtype) for n in lens])
+    vv, _, _ = fused_attn.pack_varlen([randn(n, 2, 256, dtype=dtype) for n in lens])
+    out = fused_attn.attention_varlen(qv, kv, vv, cu, cu, mx, mx, causal=True)
+    ref = orc.attention_varlen(qv.cpu(), kv.cpu(), vv.cpu(), cu.cpu(), cu.cpu(), causal=True)
+    assert max_err(out, ref) <= TOL[dtype]
+    q = randn(2, 8, 1, 256, dtype=dtype)
+    k = randn(2, 2, 3000, 256, dtype=dtype)
+    v = randn(2, 2, 3000, 256, dtype=dtype)
+    assert ops._hip_kernel_for(q, k) == "fwd"
+    out = fused_attn.attention(q, k, v)
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu())) <= TOL[dtype]
