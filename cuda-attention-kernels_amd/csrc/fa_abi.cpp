@@ -58,9 +58,9 @@ fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok, bool generi
       return fail(FA_ERR_INVALID_ARGUMENT, "k/v dtype must match q (or be float8_e4m3fn on the split-K path)");
   }
   const int d = p->head_dim;
-  if (generic_ok ? !(d == 16 || d == 32 || d == 64 || d == 128 || d == 256) : !(d == 64 || d == 128))
+  if (generic_ok ? !(d == 16 || d == 32 || d == 64 || d == 128 || d == 256) : !(d == 64 || d == 128 || d == 256))
     return fail(FA_ERR_UNSUPPORTED, generic_ok ? "head_dim must be 16, 32, 64, 128 or 256"
-                                               : "head_dim must be 64 or 128 on the split-K path");
+                                               : "head_dim must be 64, 128 or 256 on the split-K path");
   if (p->kv_dtype == FA_DTYPE_FP8_E4M3 && (p->k_scale == nullptr || p->v_scale == nullptr))
     return fail(FA_ERR_INVALID_ARGUMENT, "FP8 K/V needs k_scale and v_scale");
   if (!(p->scale == p->scale)) return fail(FA_ERR_INVALID_ARGUMENT, "scale is NaN");

@@ -51,7 +51,8 @@
 namespace fa {
 
 template <int D, class E, class KV, int NW, int BN, bool PAGED>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) attn_splitk_kernel(const TileArgs a) {
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
+attn_splitk_kernel(const TileArgs a) {
   using Shape = TileShape<D, BN>;    // 16-bit tiles
   using Shape8 = TileShape8<D, BN>;  // FP8 tiles
   constexpr bool IS_FP8 = KV::bytes == 1;
@@ -61,7 +62,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   constexpr int DB = D / 32;    // 32-wide d blocks of O^T
   // one DMA wave instruction fills 1 KiB = 64 lanes x 16 B
   constexpr int QPW = (TILE_BYTES / 1024) / NW;
-  static_assert(BN % 32 == 0 && D % 32 == 0 && (D == 64 || D == 128), "tile shape");
+  static_assert(BN % 32 == 0 && D % 32 == 0 && (D == 64 || D == 128 || D == 256), "tile shape");
   static_assert(TILE_BYTES % (1024 * NW) == 0, "tile loads must split evenly over the waves");
   static_assert(!(PAGED && IS_FP8), "paged K/V is 16-bit");
   constexpr int PG_REGS = 4;  // paged: block-table entries held per lane (64 * PG_REGS per workgroup)
@@ -211,7 +212,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   };
   // paged: descriptors of the 32-key half-tiles starting at n0 (+32); keys at or past
   // khi, and pages outside the pool, are beyond the byte limit and read as zeros
-  auto paged_resources = [&](int n0, __amdgpu_buffer_rsrc_t* rk, __amdgpu_buffer_rsrc_t* rv) {
+  auto paged_resources = [&](int n0, __amdgpu_buffer_rsrc_t* rk, __amdgpu_buffer_rsrc_t* rv) __attribute__((always_inline)) {
 #pragma unroll
     for (int h = 0; h < KB; ++h) {
       const int nh = n0 + 32 * h;
@@ -230,7 +231,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   };
 
   // ---- K/V tiles: global -> LDS (K rows permuted by kperm) ---------------------------
-  auto resources = [&](int n0, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv) {
+  auto resources = [&](int n0, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv) __attribute__((always_inline)) {
     // Byte limit = end of the tile's last key below khi.  It fits 32 bits (BN * row
     // bytes < 2^31, checked at the C ABI) and is wave-uniform, so the descriptor lives
     // in SGPRs.  Valid for any row stride, including 0 for a single-key cache.
@@ -243,7 +244,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
     rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, vlim);
   };
   // Each wave fills QPW 1-KiB blocks of the K and of the V tile straight from memory.
-  auto load_tile = [&](int n0, uint8_t* stage) {
+  auto load_tile = [&](int n0, uint8_t* stage) __attribute__((always_inline)) {
     uint8_t* kl = stage;
     uint8_t* vl = stage + TILE_BYTES;
     if constexpr (PAGED) {
@@ -348,7 +349,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 
   // One tile: prefetch tile t+1 into the other stage, then S^T, softmax, O += P V on
   // this stage.  The stage is a compile-time choice (the loop below is unrolled by 2).
-  auto tile_step = [&](auto stage_tag, int t) {
+  auto tile_step = [&](auto stage_tag, int t) __attribute__((always_inline)) {
     constexpr int ST = decltype(stage_tag)::value;
     uint8_t* cur = ST == 0 ? lds_st0 : lds_st1;
     uint8_t* nxt = ST == 0 ? lds_st1 : lds_st0;
@@ -633,8 +634,8 @@ static hipError_t launch_split_nw(const TileArgs& a, int nw, hipStream_t stream)
       return launch_splitk<D, E, KV, 1, 32, PAGED>(a, stream);
     case 2:
       return launch_splitk<D, E, KV, 2, 32, PAGED>(a, stream);
-    default:
-      return launch_splitk<D, E, KV, 4, 64, PAGED>(a, stream);
+    default:  // 64-key tiles, but 32 at D=256 (a 16-bit K or V tile stays 16 KiB)
+      return launch_splitk<D, E, KV, 4, (D == 256 ? 32 : 64), PAGED>(a, stream);
   }
 }
 
@@ -693,6 +694,8 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
     e = bf ? launch_split<128, BF16>(a, fp8, paged, nw, stream) : launch_split<128, F16>(a, fp8, paged, nw, stream);
   } else if (p.head_dim == 64) {
     e = bf ? launch_split<64, BF16>(a, fp8, paged, nw, stream) : launch_split<64, F16>(a, fp8, paged, nw, stream);
+  } else if (p.head_dim == 256) {
+    e = bf ? launch_split<256, BF16>(a, fp8, paged, nw, stream) : launch_split<256, F16>(a, fp8, paged, nw, stream);
   }
   if (e != hipSuccess) return hip_status(e, err);
 
@@ -708,6 +711,8 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
   c.n_split = S;
   if (p.head_dim == 128) {
     e = bf ? launch_combine<128, BF16>(c, out_rows, stream) : launch_combine<128, F16>(c, out_rows, stream);
+  } else if (p.head_dim == 256) {
+    e = bf ? launch_combine<256, BF16>(c, out_rows, stream) : launch_combine<256, F16>(c, out_rows, stream);
   } else {
     e = bf ? launch_combine<64, BF16>(c, out_rows, stream) : launch_combine<64, F16>(c, out_rows, stream);
   }

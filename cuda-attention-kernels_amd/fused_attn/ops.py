@@ -70,8 +70,8 @@ def is_decode_shaped(q: torch.Tensor, k: Optional[torch.Tensor]) -> bool:
     return k is not None and q.shape[-2] <= SPLITK_MAX_Q and k.shape[-2] >= SPLITK_MIN_K
 
 
-SPLITK_DTYPES = (torch.float16, torch.bfloat16)  # the split-K kernel: 16-bit Q with D in {64, 128}
-SPLITK_HEAD_DIMS = (64, 128)
+SPLITK_DTYPES = (torch.float16, torch.bfloat16)  # the split-K kernel: 16-bit Q with D in {64, 128, 256}
+SPLITK_HEAD_DIMS = (64, 128, 256)
 
 
 def _hip_kernel_for(q: torch.Tensor, k: torch.Tensor) -> str:
@@ -121,7 +121,7 @@ def default_split_len(seqlen_q: int, seqlen_k: int, batch: int = 1, heads_kv: in
     A split-K workgroup streams one partition of one (batch, kv-head) for up to 128
     (q-head, query) rows, so the grid has batch * heads_kv * row_blocks * partitions
     workgroups.  Partitions are made as long as possible while the grid keeps about
-    SPLITK_TARGET_WGS workgroups: longer partitions write fewer fp32 partials and
+    SPLITK_TARGET_WGS workgroups: longer partitions write fewer partials and
     spend less per workgroup (on MI355X, B=32 Hkv=8 n_k=32768 D=128 bf16 decode moves
     5.6 TB/s at 128-key partitions, 6.0 at 512, 6.5 at 2048 and 6.65 at 4096).
     """

@@ -110,8 +110,8 @@ size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_
                                  int32_t num_splits);
 
 /* Split-K flash-decoding: one pass per `split_len`-key partition writing
-   un-normalised fp32 partials and log2-domain statistics, then a
-   log-sum-exp combine kernel.  Replaces attention_splitk_triton
+   normalised 16-bit partials and fp32 log2-domain statistics, then a
+   log-sum-exp combine kernel.  f16/bf16 q, D in {64, 128, 256}.  Replaces attention_splitk_triton
    (fused_attn/triton_splitk.py:140-181) and, with kv_dtype ==
    FA_DTYPE_FP8_E4M3 and k_scale/v_scale set, attention_fp8_triton
    (fused_attn/fp8.py:125-147).  split_len must be a positive multiple of 64;
@@ -140,7 +140,7 @@ typedef struct fa_paged_kv {
    combine, workspace size and split_len rules) with each sequence's keys gathered
    through its block table and its own length seqlens_k[b]; p->seqlen_k is the largest
    length (it sizes the grid) and the causal mask is bottom-right per sequence.
-   f16/bf16, D in {64, 128}.  The reference lists paged K/V for its decode kernels as a
+   f16/bf16, D in {64, 128, 256}.  The reference lists paged K/V for its decode kernels as a
    roadmap item (README.md:224); the semantics are those of attention_splitk_triton
    (fused_attn/triton_splitk.py:140-181) applied to each sequence's gathered keys. */
 fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* kv, int32_t split_len,

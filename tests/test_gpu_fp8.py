@@ -27,7 +27,8 @@ def test_fp8_kernel_matches_dequantized_oracle_prefill_shaped():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k,d", [(2, 8, 2, 1, 1000, 128), (1, 4, 4, 3, 4096, 64),
-                                                  (3, 16, 2, 16, 2100, 128), (1, 4, 1, 200, 333, 128)])
+                                                  (3, 16, 2, 16, 2100, 128), (1, 4, 1, 200, 333, 128),
+                                                  (2, 8, 2, 4, 1300, 256)])
 @pytest.mark.parametrize("split_len", [None, 64, 256])
 def test_fp8_matches_oracle(b, h_q, h_kv, n_q, n_k, d, causal, dtype, split_len):
     announce(f"fp8 b={b} hq={h_q} hkv={h_kv} nq={n_q} nk={n_k} d={d} causal={causal} {dtype} split={split_len}")

@@ -61,7 +61,7 @@ def test_fuzz_dense(seed):
 def test_fuzz_splitk(seed):
     rng = random.Random(1000 + seed)
     dtype = rng.choice([torch.bfloat16, torch.float16])
-    d = rng.choice([64, 128])
+    d = rng.choice([64, 128, 256])
     hkv = rng.choice([1, 2, 8])
     hq = hkv * rng.choice([1, 4, 8])
     b = rng.randint(1, 4)
@@ -83,7 +83,7 @@ def test_fuzz_splitk(seed):
 @pytest.mark.parametrize("seed", range(8))
 def test_fuzz_fp8_splitk(seed):
     rng = random.Random(2000 + seed)
-    d = rng.choice([64, 128])
+    d = rng.choice([64, 128, 256])
     hkv = rng.choice([1, 4])
     hq = hkv * rng.choice([1, 8])
     b = rng.randint(1, 3)
@@ -130,7 +130,7 @@ def test_fuzz_varlen(seed):
 def test_fuzz_paged(seed):
     rng = random.Random(4000 + seed)
     dtype = rng.choice([torch.bfloat16, torch.float16])
-    d = rng.choice([64, 128])
+    d = rng.choice([64, 128, 256])
     page = rng.choice([32, 64, 96, 128])
     hkv = rng.choice([1, 2, 4])
     hq = hkv * rng.choice([1, 4])

@@ -26,7 +26,7 @@ def _dense_and_paged(b, hq, hkv, nq, n, d, page, dtype, lens=None, seed=0, extra
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("page", [32, 64, 256])
 @pytest.mark.parametrize("nq,causal", [(1, False), (4, True), (20, True)])
 def test_paged_matches_oracle(dtype, d, page, nq, causal):

@@ -16,7 +16,8 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("num_splits", [1, 3, 8])
 @pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k,d",
                          [(1, 2, 1, 1, 1000, 64), (2, 4, 2, 4, 777, 64), (1, 2, 2, 16, 2048, 128),
-                          (2, 32, 8, 1, 3000, 128), (1, 8, 1, 16, 2500, 128)])
+                          (2, 32, 8, 1, 3000, 128), (1, 8, 1, 16, 2500, 128),
+                          (2, 8, 2, 1, 1500, 256), (1, 4, 1, 16, 900, 256)])
 def test_splitk_matches_oracle(b, h_q, h_kv, n_q, n_k, d, num_splits, causal, dtype):
     announce(f"splitk b={b} hq={h_q} hkv={h_kv} nq={n_q} nk={n_k} d={d} S={num_splits} causal={causal} {dtype}")
     torch.manual_seed(0)
