@@ -16,7 +16,7 @@ struct TileArgs {
   const void* q;
   const void* k;
   const void* v;
-  void* o;     // prefill: output in the q dtype; split-K: fp32 partials [rows, S, D]
+  void* o;     // prefill: output in the q dtype; split-K: 16-bit partials [rows, S, D]
   float* ml;   // split-K: (max, sum) pairs [rows, S, 2]
   float* lse;  // prefill: optional natural-log LSE
   const float* k_scale;
@@ -32,6 +32,7 @@ struct TileArgs {
   int32_t n_split, split_len;
   int32_t ppw, n_chunk;  // split-K: partitions per workgroup, workgroups per (b, kv-head, row block)
   int32_t total;  // workgroups in the grid
+  int32_t kv_groups;  // prefill: (batch, kv-head) pairs
   float qk_scale; // softmax scale * log2(e)
   int32_t causal;
   int32_t varlen;

@@ -71,15 +71,25 @@ attn_fwd_kernel(const TileArgs a) {
   //
   // Varlen batches are the exception: their sequences differ in length, and ranges of
   // whole sequences per XCD load the XCDs unevenly (measured: a 16-sequence batch ran at
-  // 0.18 of peak).  There the blocks go rank-major over all (sequence, q-head) pairs in
-  // launch order, heaviest ranks first, and the dispatcher spreads them over the XCDs.
+  // 0.18 of peak).  There the order is rank-major per XCD: the dispatcher deals workgroups
+  // to the XCDs round-robin (blockIdx % 8), XCD x takes the (sequence, kv-head) groups
+  // g = x (mod 8) and walks them rank by rank, heaviest causal ranks first, with the q-heads
+  // of one kv-head side by side, so they run together and read its K/V through one L2
+  // (measured: +8-10% over rank-major across all XCDs, which fetched each K/V tile into up
+  // to four L2s).  The host pads the grid to a multiple of 8 groups; padding exits here.
   constexpr int64_t kL2UnitBytes = int64_t{4} << 20;
-  const int nbh = a.total / a.n_rowblk;  // (batch, q-head) pairs
+  constexpr int kXcds = 8;
   int mrev, item;
   if (a.varlen) {
-    mrev = (int)blockIdx.x / nbh;
-    item = (int)blockIdx.x % nbh;
+    const int xcd = (int)blockIdx.x % kXcds, local = (int)blockIdx.x / kXcds;
+    const int per_rank = a.total / (a.n_rowblk * kXcds);  // this XCD's (group, q-head) items per rank
+    mrev = local / per_rank;
+    const int j = local % per_rank;
+    const int kvg = (j / a.group) * kXcds + xcd;
+    if (kvg >= a.kv_groups) return;  // grid padding (uniform over the workgroup)
+    item = kvg * a.group + j % a.group;
   } else {
+    const int nbh = a.total / a.n_rowblk;  // (batch, q-head) pairs
     const int logical = xcd_remap((int)blockIdx.x, a.total);
     const int64_t kv_head_bytes = (int64_t)max(a.nk, 1) * D * 2 * 2;
     const int unit_heads = max(1, (int)(kL2UnitBytes / kv_head_bytes)) * a.group;
@@ -454,12 +464,16 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
   }
   if (a.nq <= 0 || p.batch <= 0) return FA_OK;
   a.n_rowblk = (a.nq + 127) / 128;
-  const int64_t total = (int64_t)p.batch * p.heads_q * a.n_rowblk;
+  const int64_t kv_groups = (int64_t)p.batch * p.heads_kv;
+  // varlen: the (sequence, kv-head) groups are padded to a multiple of the 8 XCDs
+  const int64_t groups = varlen ? (kv_groups + 7) / 8 * 8 : kv_groups;
+  const int64_t total = groups * a.group * a.n_rowblk;
   if (total > INT32_MAX) {
     *err = "grid too large";
     return FA_ERR_UNSUPPORTED;
   }
   a.total = (int32_t)total;
+  a.kv_groups = (int32_t)kv_groups;
   a.n_split = 1;
   a.split_len = 0;
   hipError_t e = hipErrorInvalidValue;

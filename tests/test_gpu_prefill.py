@@ -157,7 +157,8 @@ def test_baseline_prefill_configs(cfg):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_head_dim_256_views_varlen_and_decode_shapes(dtype):
     """D=256 on the MFMA kernel (32-key tiles, one wave per SIMD): the [B,N,H,D] view, a
-    varlen batch with an empty sequence, and a decode-shaped call (split-K takes D<=128)."""
+    varlen batch with an empty sequence, and a decode-shaped call (split-K, and the prefill kernel on
+    the same shape)."""
     announce(f"d=256 extra shapes {dtype}")
     torch.manual_seed(0)
     x = randn(2, 150, 3, 4, 256, dtype=dtype)
@@ -174,6 +175,8 @@ def test_head_dim_256_views_varlen_and_decode_shapes(dtype):
     q = randn(2, 8, 1, 256, dtype=dtype)
     k = randn(2, 2, 3000, 256, dtype=dtype)
     v = randn(2, 2, 3000, 256, dtype=dtype)
-    assert ops._hip_kernel_for(q, k) == "fwd"
+    assert ops._hip_kernel_for(q, k) == "splitk"
     out = fused_attn.attention(q, k, v)
-    assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu())) <= TOL[dtype]
+    ref = orc.attention(q.cpu(), k.cpu(), v.cpu())
+    assert max_err(out, ref) <= TOL[dtype]
+    assert max_err(_hip.fwd(q, k, v), ref) <= TOL[dtype]
