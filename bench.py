@@ -204,6 +204,33 @@ def bench_decode(steps, warmup, only_128=False):
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
             "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
         }
+    del q, k8, ks, v8, vs
+    torch.cuda.empty_cache()
+    res.update(bench_decode_d256(steps, warmup, g))
+    return res
+
+
+def bench_decode_d256(steps, warmup, g):
+    """Split-K decode at head dim 256: B=8 Hq=32 Hkv=8 n_k=32768 bf16 (2.147 GB of K+V), 128-key partitions."""
+    import torch
+
+    import fused_attn
+
+    b, hq, hkv, nk, d = 8, 32, 8, 32768, 256
+    k = torch.randn(b, hkv, nk, d, device="cuda", generator=g).bfloat16()
+    v = torch.randn(b, hkv, nk, d, device="cuda", generator=g).bfloat16()
+    q = torch.randn(b, hq, 1, d, device="cuda", generator=g).bfloat16()
+    fn = lambda: fused_attn.attention_splitk(q, k, v, split_len=128)  # noqa: E731
+    wall, ev = _time_calls(fn, steps, warmup)
+    nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
+    res = {"decode_d256": {
+        "workload": f"split-K B={b} Hq={hq} Hkv={hkv} n_q=1 n_k={nk} D={d} bf16, 128-key partitions + LSE combine",
+        "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+        "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+    }}
+    del q, k, v
+    torch.cuda.empty_cache()
     return res
 
 
