@@ -50,7 +50,16 @@
 
 namespace fa {
 
-template <int D, class E, class KV, int NW, int BN, bool PAGED>
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits 3:0 and 15:14), other counters unconstrained.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+// s_waitcnt lgkmcnt(0), other counters unconstrained.
+__device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+template <int D, class E, class KV, int NW, int BN, bool PAGED, bool ONE_STAGE>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 attn_splitk_kernel(const TileArgs a) {
   using Shape = TileShape<D, BN>;    // 16-bit tiles
@@ -68,12 +77,19 @@ attn_splitk_kernel(const TileArgs a) {
   constexpr int PG_REGS = 4;  // paged: block-table entries held per lane (64 * PG_REGS per workgroup)
   constexpr float NEG_INF = -__builtin_inff();
 
-  // Two LDS stages (K tile, then V tile) as separate arrays: every access names its
-  // stage at compile time, so the compiler can tell that the DMA filling one stage
-  // never aliases reads of the other (and does not wait for the prefetch before
-  // reading the current tile).
-  __shared__ __align__(16) uint8_t lds_st0[2 * TILE_BYTES];
-  __shared__ __align__(16) uint8_t lds_st1[2 * TILE_BYTES];
+  // Two LDS stages (tile t+1 loads while tile t is read), or, for one-wave workgroups, a
+  // single stage: K and V in arrays of their own, each refilled as soon as it has been
+  // read.  That halves the LDS of a workgroup, so more fit on a CU; it pays where LDS
+  // rather than registers bounds the occupancy (chosen at launch).  Every buffer is an
+  // array of its own and every access names it at compile time, so the compiler can tell
+  // that a DMA filling one buffer never aliases reads of another (and does not wait for
+  // that DMA before reading).
+  static_assert(!ONE_STAGE || NW == 1, "single stage is for one-wave workgroups");
+  constexpr int STAGES = ONE_STAGE ? 1 : 2;
+  __shared__ __align__(16) uint8_t lds_st0[STAGES == 2 ? 2 * TILE_BYTES : 16];
+  __shared__ __align__(16) uint8_t lds_st1[STAGES == 2 ? 2 * TILE_BYTES : 16];
+  __shared__ __align__(16) uint8_t lds_k1[STAGES == 1 ? TILE_BYTES : 16];
+  __shared__ __align__(16) uint8_t lds_v1[STAGES == 1 ? TILE_BYTES : 16];
 
   // ---- work item: (batch, kv-head, chunk of ppw partitions, row block) -------------
   const int logical = xcd_remap((int)blockIdx.x, a.total);
@@ -244,9 +260,7 @@ attn_splitk_kernel(const TileArgs a) {
     rv = make_rsrc(vbase + (int64_t)n0 * vrow_bytes, vlim);
   };
   // Each wave fills QPW 1-KiB blocks of the K and of the V tile straight from memory.
-  auto load_tile = [&](int n0, uint8_t* stage) __attribute__((always_inline)) {
-    uint8_t* kl = stage;
-    uint8_t* vl = stage + TILE_BYTES;
+  auto load_parts = [&](int n0, uint8_t* kl, uint8_t* vl, bool do_k, bool do_v) __attribute__((always_inline)) {
     if constexpr (PAGED) {
       __amdgpu_buffer_rsrc_t rk[KB], rv[KB];
       paged_resources(n0, rk, rv);
@@ -259,8 +273,8 @@ attn_splitk_kernel(const TileArgs a) {
         const int half = (blk * 1024 / (D * KV::bytes)) / 32;
         const __amdgpu_buffer_rsrc_t ck = (KB > 1 && half) ? rk[KB - 1] : rk[0];
         const __amdgpu_buffer_rsrc_t cv = (KB > 1 && half) ? rv[KB - 1] : rv[0];
-        lds_dma16<true>(ck, kl + blk * 1024, (kperm(r) - 32 * half) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16));
-        lds_dma16<true>(cv, vl + blk * 1024, (r - 32 * half) * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16));
+        if (do_k) lds_dma16<true>(ck, kl + blk * 1024, (kperm(r) - 32 * half) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16));
+        if (do_v) lds_dma16<true>(cv, vl + blk * 1024, (r - 32 * half) * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16));
       }
       return;
     }
@@ -273,9 +287,12 @@ attn_splitk_kernel(const TileArgs a) {
       const int r = byte / (D * KV::bytes), p = (byte % (D * KV::bytes)) / 16;
       const int sk = IS_FP8 ? Shape8::swz_k(r) : Shape::swz_k(r);
       const int sv = IS_FP8 ? Shape8::swz_v(r) : Shape::swz_v(r);
-      lds_dma16<true>(rk, kl + blk * 1024, kperm(r) * (int)krow_bytes + ((p ^ sk) * 16));
-      lds_dma16<true>(rv, vl + blk * 1024, r * (int)vrow_bytes + ((p ^ sv) * 16));
+      if (do_k) lds_dma16<true>(rk, kl + blk * 1024, kperm(r) * (int)krow_bytes + ((p ^ sk) * 16));
+      if (do_v) lds_dma16<true>(rv, vl + blk * 1024, r * (int)vrow_bytes + ((p ^ sv) * 16));
     }
+  };
+  auto load_tile = [&](int n0, uint8_t* stage) __attribute__((always_inline)) {
+    load_parts(n0, stage, stage + TILE_BYTES, true, true);
   };
   f32x16 oacc[DB];
 #pragma unroll
@@ -343,48 +360,37 @@ attn_splitk_kernel(const TileArgs a) {
     l_run = 0.f;
   };
 
-  if (n_tiles > 0) load_tile(klo, lds_st0);
-  lds_dma_wait();
-  __syncthreads();
+  // The K and V tiles the compute below reads (set per tile; constant after unrolling).
+  const uint8_t* Ks = lds_st0;
+  const uint8_t* Vs = lds_st0 + TILE_BYTES;
+    // MFMA A operands from LDS (FP8 widened to E on the way)
+    auto k_operand = [&](int kb, int s) __attribute__((always_inline)) {
+      if constexpr (IS_FP8) {
+        const u32x2 raw = ld8(Ks + kb * 32 * D + koffs8[s]);
+        const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        return ld16((const uint16_t*)Ks + kb * 32 * D + koffs[s]);
+      }
+    };
+    auto v_operand = [&](int kb, int h, int d) __attribute__((always_inline)) {
+      if constexpr (IS_FP8) {
+        const u32x2 raw = lds_read_tr8(Vs + (kb * 32 + 16 * h) * D + voffs8[d]);
+        const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        const uint16_t* vp = (const uint16_t*)Vs + (kb * 32 + 16 * h) * D;
+        const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
+        const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+    };
 
-  // One tile: prefetch tile t+1 into the other stage, then S^T, softmax, O += P V on
-  // this stage.  The stage is a compile-time choice (the loop below is unrolled by 2).
-  auto tile_step = [&](auto stage_tag, int t) __attribute__((always_inline)) {
-    constexpr int ST = decltype(stage_tag)::value;
-    uint8_t* cur = ST == 0 ? lds_st0 : lds_st1;
-    uint8_t* nxt = ST == 0 ? lds_st1 : lds_st0;
-    const int n0 = klo + t * BN;
-    if (t + 1 < n_tiles) load_tile(n0 + BN, nxt);  // released by the previous barrier
 
-    if (wave_active && n0 < wave_khi) {
-      const uint8_t* Ks = cur;
-      const uint8_t* Vs = cur + TILE_BYTES;
-      // MFMA A operands from LDS (FP8 widened to E on the way)
-      auto k_operand = [&](int kb, int s) __attribute__((always_inline)) {
-        if constexpr (IS_FP8) {
-          const u32x2 raw = ld8(Ks + kb * 32 * D + koffs8[s]);
-          const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
-          return u32x4{lo[0], lo[1], hi[0], hi[1]};
-        } else {
-          return ld16((const uint16_t*)Ks + kb * 32 * D + koffs[s]);
-        }
-      };
-      auto v_operand = [&](int kb, int h, int d) __attribute__((always_inline)) {
-        if constexpr (IS_FP8) {
-          const u32x2 raw = lds_read_tr8(Vs + (kb * 32 + 16 * h) * D + voffs8[d]);
-          const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
-          return u32x4{lo[0], lo[1], hi[0], hi[1]};
-        } else {
-          const uint16_t* vp = (const uint16_t*)Vs + (kb * 32 + 16 * h) * D;
-          const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
-          const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
-          return u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
-      };
-
-      // S^T = K Q^T.  The KB accumulation chains are independent; stepping them
-      // together keeps the MFMA pipe fed while each chain's last result is in flight.
-      f32x16 sacc[KB];
+  // S^T = K Q^T of one tile.
+  auto tile_qk = [&](f32x16(&sacc)[KB]) __attribute__((always_inline)) {
+    // The KB accumulation chains are independent; stepping them
+    // together keeps the MFMA pipe fed while each chain's last result is in flight.
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) sacc[kb] = f32x16{};
       __builtin_amdgcn_s_setprio(1);
@@ -394,6 +400,9 @@ attn_splitk_kernel(const TileArgs a) {
         for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32<E>(k_operand(kb, s), qf[s], sacc[kb]);
       }
       __builtin_amdgcn_s_setprio(0);
+  };
+  // Scale, mask, online softmax and O += V P of the tile at n0.
+  auto tile_softmax_pv = [&](f32x16(&sacc)[KB], int n0) __attribute__((always_inline)) {
 
       // per-block score scale (FP8: times the block's k_scale, fp8.py:104)
       float sc[KB], vs[KB];
@@ -490,18 +499,75 @@ attn_splitk_kernel(const TileArgs a) {
         }
       }
       __builtin_amdgcn_s_setprio(0);
-    }
-    if (t + 1 < n_tiles) lds_dma_wait();
-    __syncthreads();
-    // The last tile of a partition closes it.  Its stores are issued after this
-    // tile's wait: vmcnt counts stores too, so they complete under the next tile
-    // instead of stalling this one.
-    if ((t + 1) % tiles_per_part == 0 || t + 1 == n_tiles) emit_partial(part0 + t / tiles_per_part);
   };
-  for (int t = 0; t < n_tiles; t += 2) {
-    tile_step(std::integral_constant<int, 0>{}, t);
-    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
+
+  if constexpr (STAGES == 2) {
+    if (n_tiles > 0) load_tile(klo, lds_st0);
+    lds_dma_wait();
+    __syncthreads();
+
+    // One tile: prefetch tile t+1 into the other stage, then S^T, softmax, O += P V on
+    // this stage.  The stage is a compile-time choice (the loop below is unrolled by 2).
+    auto tile_step = [&](auto stage_tag, int t) __attribute__((always_inline)) {
+      constexpr int ST = decltype(stage_tag)::value;
+      uint8_t* cur = ST == 0 ? lds_st0 : lds_st1;
+      uint8_t* nxt = ST == 0 ? lds_st1 : lds_st0;
+      const int n0 = klo + t * BN;
+      if (t + 1 < n_tiles) load_tile(n0 + BN, nxt);  // released by the previous barrier
+      if (wave_active && n0 < wave_khi) {
+        Ks = cur;
+        Vs = cur + TILE_BYTES;
+        f32x16 sacc[KB];
+        tile_qk(sacc);
+        tile_softmax_pv(sacc, n0);
+      }
+      if (t + 1 < n_tiles) lds_dma_wait();
+      __syncthreads();
+      // The last tile of a partition closes it.  Its stores are issued after this
+      // tile's wait: vmcnt counts stores too, so they complete under the next tile
+      // instead of stalling this one.
+      if ((t + 1) % tiles_per_part == 0 || t + 1 == n_tiles) emit_partial(part0 + t / tiles_per_part);
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+      tile_step(std::integral_constant<int, 0>{}, t);
+      if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
+    }
+  } else {
+    // Single stage: K_{t+1} is fetched as soon as S_t has been computed, V_{t+1} as soon
+    // as O has taken V_t, so about one tile is in flight while the other half is read.
+    // vmcnt counts this wave's loads and stores in issue order: waiting for it to drop
+    // to QPW leaves only the QPW DMA instructions issued last in flight.
+    Ks = lds_k1;
+    Vs = lds_v1;
+    if (n_tiles > 0) load_parts(klo, lds_k1, lds_v1, true, true);
+    lds_dma_wait();
+    __syncthreads();
+    for (int t = 0; t < n_tiles; ++t) {
+      const int n0 = klo + t * BN;
+      const bool act = wave_active && n0 < wave_khi;
+      vm_wait<QPW>();  // K_t landed (issued before V_t's QPW instructions)
+      __syncthreads();
+      f32x16 sacc[KB];
+      if (act) tile_qk(sacc);
+      if (t + 1 < n_tiles) {
+        lgkm_wait0();  // this wave's K reads have returned
+        __syncthreads();
+        load_parts(n0 + BN, lds_k1, lds_v1, true, false);
+        vm_wait<QPW>();  // V_t landed (issued before K_{t+1}'s QPW instructions)
+      } else {
+        lds_dma_wait();
+      }
+      __syncthreads();
+      if (act) tile_softmax_pv(sacc, n0);
+      if ((t + 1) % tiles_per_part == 0 || t + 1 == n_tiles) emit_partial(part0 + t / tiles_per_part);
+      if (t + 1 < n_tiles) {
+        lgkm_wait0();  // this wave's V reads have returned
+        __syncthreads();
+        load_parts(n0 + BN, lds_k1, lds_v1, false, true);
+      }
+    }
   }
+
   // partitions past the visible keys (causal, or past the sequence end): empty
   // partials, m = -inf and l = 0, which the combine weighs by zero
   for (int part = part0 + (n_tiles + tiles_per_part - 1) / tiles_per_part; part < part_end; ++part) emit_partial(part);
@@ -575,10 +641,10 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
 // Host-side launchers
 // ------------------------------------------------------------------------------------
 
-template <int D, class E, class KV, int NW, int BN, bool PAGED>
+template <int D, class E, class KV, int NW, int BN, bool PAGED, bool ONE_STAGE = false>
 static hipError_t launch_splitk(const TileArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_splitk_kernel<D, E, KV, NW, BN, PAGED>), dim3((unsigned)a.total), dim3(NW * 64), 0, stream,
-                     a);
+  hipLaunchKernelGGL((attn_splitk_kernel<D, E, KV, NW, BN, PAGED, ONE_STAGE>), dim3((unsigned)a.total), dim3(NW * 64),
+                     0, stream, a);
   return hipGetLastError();
 }
 
@@ -631,6 +697,13 @@ template <int D, class E, class KV, bool PAGED>
 static hipError_t launch_split_nw(const TileArgs& a, int nw, hipStream_t stream) {
   switch (nw) {
     case 1:
+      // Single LDS stage for 16-bit K/V where two stages cap the workgroups per CU by LDS:
+      // D=256 (2 -> 4 per CU; measured +15% at 128-key partitions) and D=128 with
+      // partitions of 512 keys or more (5 -> 8 per CU; +1.3-2.7%; at 128 keys the longer
+      // per-tile wait costs 1.2% instead).  FP8 tiles are small enough already.
+      if constexpr (KV::bytes == 2 && D >= 128) {
+        if (D == 256 || a.split_len >= 512) return launch_splitk<D, E, KV, 1, 32, PAGED, true>(a, stream);
+      }
       return launch_splitk<D, E, KV, 1, 32, PAGED>(a, stream);
     case 2:
       return launch_splitk<D, E, KV, 2, 32, PAGED>(a, stream);
