@@ -697,12 +697,13 @@ template <int D, class E, class KV, bool PAGED>
 static hipError_t launch_split_nw(const TileArgs& a, int nw, hipStream_t stream) {
   switch (nw) {
     case 1:
-      // Single LDS stage for 16-bit K/V where two stages cap the workgroups per CU by LDS:
-      // D=256 (2 -> 4 per CU; measured +15% at 128-key partitions) and D=128 with
-      // partitions of 512 keys or more (5 -> 8 per CU; +1.3-2.7%; at 128 keys the longer
+      // Single LDS stage for 16-bit K/V where two stages cap the workgroups per CU by LDS
+      // (measured on the 32k-key decode cache): D=64 (10 -> 16 per CU; +4.6% at 128-key
+      // partitions, +1.4% at 4096), D=256 (2 -> 4; +15% at 128-key partitions) and D=128
+      // with partitions of 512 keys or more (5 -> 8; +1.3-2.7%; at 128 keys the longer
       // per-tile wait costs 1.2% instead).  FP8 tiles are small enough already.
-      if constexpr (KV::bytes == 2 && D >= 128) {
-        if (D == 256 || a.split_len >= 512) return launch_splitk<D, E, KV, 1, 32, PAGED, true>(a, stream);
+      if constexpr (KV::bytes == 2) {
+        if (D != 128 || a.split_len >= 512) return launch_splitk<D, E, KV, 1, 32, PAGED, true>(a, stream);
       }
       return launch_splitk<D, E, KV, 1, 32, PAGED>(a, stream);
     case 2:
