@@ -363,142 +363,140 @@ attn_splitk_kernel(const TileArgs a) {
   // The K and V tiles the compute below reads (set per tile; constant after unrolling).
   const uint8_t* Ks = lds_st0;
   const uint8_t* Vs = lds_st0 + TILE_BYTES;
-    // MFMA A operands from LDS (FP8 widened to E on the way)
-    auto k_operand = [&](int kb, int s) __attribute__((always_inline)) {
-      if constexpr (IS_FP8) {
-        const u32x2 raw = ld8(Ks + kb * 32 * D + koffs8[s]);
-        const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
-      } else {
-        return ld16((const uint16_t*)Ks + kb * 32 * D + koffs[s]);
-      }
-    };
-    auto v_operand = [&](int kb, int h, int d) __attribute__((always_inline)) {
-      if constexpr (IS_FP8) {
-        const u32x2 raw = lds_read_tr8(Vs + (kb * 32 + 16 * h) * D + voffs8[d]);
-        const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
-      } else {
-        const uint16_t* vp = (const uint16_t*)Vs + (kb * 32 + 16 * h) * D;
-        const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
-        const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
-    };
-
+  // MFMA A operands from LDS (FP8 widened to E on the way)
+  auto k_operand = [&](int kb, int s) __attribute__((always_inline)) {
+    if constexpr (IS_FP8) {
+      const u32x2 raw = ld8(Ks + kb * 32 * D + koffs8[s]);
+      const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    } else {
+      return ld16((const uint16_t*)Ks + kb * 32 * D + koffs[s]);
+    }
+  };
+  auto v_operand = [&](int kb, int h, int d) __attribute__((always_inline)) {
+    if constexpr (IS_FP8) {
+      const u32x2 raw = lds_read_tr8(Vs + (kb * 32 + 16 * h) * D + voffs8[d]);
+      const u32x2 lo = fp8x4_to_e<E>(raw[0]), hi = fp8x4_to_e<E>(raw[1]);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    } else {
+      const uint16_t* vp = (const uint16_t*)Vs + (kb * 32 + 16 * h) * D;
+      const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
+      const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
 
   // S^T = K Q^T of one tile.
   auto tile_qk = [&](f32x16(&sacc)[KB]) __attribute__((always_inline)) {
-    // The KB accumulation chains are independent; stepping them
-    // together keeps the MFMA pipe fed while each chain's last result is in flight.
+    // The KB accumulation chains are independent; stepping them together keeps the MFMA
+    // pipe fed while each chain's last result is in flight.
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) sacc[kb] = f32x16{};
-      __builtin_amdgcn_s_setprio(1);
+    for (int kb = 0; kb < KB; ++kb) sacc[kb] = f32x16{};
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
+    for (int s = 0; s < KS; ++s) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32<E>(k_operand(kb, s), qf[s], sacc[kb]);
-      }
-      __builtin_amdgcn_s_setprio(0);
+      for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32<E>(k_operand(kb, s), qf[s], sacc[kb]);
+    }
+    __builtin_amdgcn_s_setprio(0);
   };
   // Scale, mask, online softmax and O += V P of the tile at n0.
   auto tile_softmax_pv = [&](f32x16(&sacc)[KB], int n0) __attribute__((always_inline)) {
+    // per-block score scale (FP8: times the block's k_scale, fp8.py:104)
+    float sc[KB], vs[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      if constexpr (KV::bytes == 1) {
+        const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
+        sc[kb] = fmaxf(c_abs * ksc[blk], kMinScale);
+        vs[kb] = vsc[blk];
+      } else {
+        sc[kb] = c_abs;
+        vs[kb] = 1.f;
+      }
+    }
 
-      // per-block score scale (FP8: times the block's k_scale, fp8.py:104)
-      float sc[KB], vs[KB];
+    // Masked tiles (the causal diagonal, the key tail) set excluded scores to -inf
+    // in one uniform block; exp2 then gives 0 for them, so the softmax below is the
+    // same straight-line code for every tile.
+    if (n0 + BN > mask_from) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+          const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
+          sacc[kb][r] = ok ? sacc[kb][r] : NEG_INF;
+        }
+      }
+    }
+
+    // tile max of the scaled scores (sc > 0: max of sc*s is sc*max(s))
+    float mt = NEG_INF;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      float mx = sacc[kb][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = vmax(mx, sacc[kb][r]);
+      mt = vmax(mt, mx * sc[kb]);
+    }
+    mt = max_xor32(mt);
+
+    // Lazy rescale: keep the running max unless some row of the wave grew by
+    // more than 2^8; p = 2^(c*s - m_run) then stays <= 256 (no overflow risk),
+    // and O, l stay consistent because both use the same m_run.
+    const float m_new = vmax(m_run, mt);
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
+      const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - m_safe_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+      m_run = m_new;
+    }
+    const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
+
+    // P = 2^(c*s - m) as 16-bit B operands of PV
+    u32x4 pf[KB][2];
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(sacc[kb][r], sc[kb], -m_safe));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
         if constexpr (KV::bytes == 1) {
-          const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
-          sc[kb] = fmaxf(c_abs * ksc[blk], kMinScale);
-          vs[kb] = vsc[blk];
+          // v_scale folded into P (the reference scales P.V by v_scale, fp8.py:116)
+          const float v = vs[kb];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
+          pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0] * v, p[8 * h + 1] * v), pack2<E>(p[8 * h + 2] * v, p[8 * h + 3] * v),
+                            pack2<E>(p[8 * h + 4] * v, p[8 * h + 5] * v), pack2<E>(p[8 * h + 6] * v, p[8 * h + 7] * v)};
         } else {
-          sc[kb] = c_abs;
-          vs[kb] = 1.f;
+          pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0], p[8 * h + 1]), pack2<E>(p[8 * h + 2], p[8 * h + 3]),
+                            pack2<E>(p[8 * h + 4], p[8 * h + 5]), pack2<E>(p[8 * h + 6], p[8 * h + 7])};
+          // the row sum of the rounded P that the MFMA consumes (so O/l is a convex combination)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rs = sum2<E>(pf[kb][h][e], rs);
         }
       }
+    }
+    l_run += rs;
 
-      // Masked tiles (the causal diagonal, the key tail) set excluded scores to -inf
-      // in one uniform block; exp2 then gives 0 for them, so the softmax below is the
-      // same straight-line code for every tile.
-      if (n0 + BN > mask_from) {
+    // O^T += V^T P^T
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int n = n0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
-            const bool ok = (n < khi) & ((a.causal == 0) | (n <= qlim));
-            sacc[kb][r] = ok ? sacc[kb][r] : NEG_INF;
-          }
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {  // DB independent chains per 16-key step
+          oacc[d] = mfma32<E>(v_operand(kb, h, d), pf[kb][h], oacc[d]);
         }
       }
-
-      // tile max of the scaled scores (sc > 0: max of sc*s is sc*max(s))
-      float mt = NEG_INF;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        float mx = sacc[kb][0];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) mx = vmax(mx, sacc[kb][r]);
-        mt = vmax(mt, mx * sc[kb]);
-      }
-      mt = max_xor32(mt);
-
-      // Lazy rescale: keep the running max unless some row of the wave grew by
-      // more than 2^8; p = 2^(c*s - m_run) then stays <= 256 (no overflow risk),
-      // and O, l stay consistent because both use the same m_run.
-      const float m_new = vmax(m_run, mt);
-      if (__builtin_amdgcn_ballot_w64(m_new > m_run + kRescaleLog2) != 0) {
-        const float m_safe_new = (m_new == NEG_INF) ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run - m_safe_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
-        m_run = m_new;
-      }
-      const float m_safe = (m_run == NEG_INF) ? 0.f : m_run;
-
-      // P = 2^(c*s - m) as 16-bit B operands of PV
-      u32x4 pf[KB][2];
-      float rs = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        float p[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(__builtin_fmaf(sacc[kb][r], sc[kb], -m_safe));
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          if constexpr (KV::bytes == 1) {
-            // v_scale folded into P (the reference scales P.V by v_scale, fp8.py:116)
-            const float v = vs[kb];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
-            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0] * v, p[8 * h + 1] * v), pack2<E>(p[8 * h + 2] * v, p[8 * h + 3] * v),
-                              pack2<E>(p[8 * h + 4] * v, p[8 * h + 5] * v), pack2<E>(p[8 * h + 6] * v, p[8 * h + 7] * v)};
-          } else {
-            pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0], p[8 * h + 1]), pack2<E>(p[8 * h + 2], p[8 * h + 3]),
-                              pack2<E>(p[8 * h + 4], p[8 * h + 5]), pack2<E>(p[8 * h + 6], p[8 * h + 7])};
-            // the row sum of the rounded P that the MFMA consumes (so O/l is a convex combination)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) rs = sum2<E>(pf[kb][h][e], rs);
-          }
-        }
-      }
-      l_run += rs;
-
-      // O^T += V^T P^T
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-          for (int d = 0; d < DB; ++d) {  // DB independent chains per 16-key step
-            oacc[d] = mfma32<E>(v_operand(kb, h, d), pf[kb][h], oacc[d]);
-          }
-        }
-      }
-      __builtin_amdgcn_s_setprio(0);
+    }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   if constexpr (STAGES == 2) {
