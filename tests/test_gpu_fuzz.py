@@ -33,7 +33,7 @@ def _tensor(shape, dtype, bnhd):
     return randn(b, n, h, d, dtype=dtype).transpose(1, 2)
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_fuzz_dense(seed):
     rng = random.Random(seed)
     dtype, d = rng.choice([(torch.bfloat16, 64), (torch.bfloat16, 128), (torch.float16, 64), (torch.float16, 128),
@@ -57,7 +57,7 @@ def test_fuzz_dense(seed):
     assert max_err(out, ref) <= _tol(dtype)
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(32))
 def test_fuzz_splitk(seed):
     rng = random.Random(1000 + seed)
     dtype = rng.choice([torch.bfloat16, torch.float16])
@@ -80,7 +80,7 @@ def test_fuzz_splitk(seed):
     assert max_err(out, ref) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_fuzz_fp8_splitk(seed):
     rng = random.Random(2000 + seed)
     d = rng.choice([64, 128, 256])
@@ -100,7 +100,7 @@ def test_fuzz_fp8_splitk(seed):
     assert max_err(out, ref) <= FP8_TOL
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(24))
 def test_fuzz_varlen(seed):
     rng = random.Random(3000 + seed)
     dtype, d = rng.choice([(torch.bfloat16, 128), (torch.float16, 64), (torch.bfloat16, 32), (torch.float32, 64)])
@@ -126,7 +126,7 @@ def test_fuzz_varlen(seed):
     assert max_err(out, ref) <= _tol(dtype)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_fuzz_paged(seed):
     rng = random.Random(4000 + seed)
     dtype = rng.choice([torch.bfloat16, torch.float16])

@@ -120,6 +120,40 @@ def test_varlen_lse(lens, causal):
         assert (g[fin] - ref[fin]).abs().max().item() < 2.0 ** -8
 
 
+@pytest.mark.parametrize("nseq,h_kv", [(1, 1), (3, 2), (4, 2), (5, 2), (9, 1), (4, 4), (17, 1)])
+def test_varlen_group_counts_around_the_xcd_multiple(nseq, h_kv):
+    """The varlen grid walks (sequence, kv-head) groups per XCD and is padded to a multiple of 8 groups:
+    group counts below, at and above multiples of 8 (1, 6, 8, 10, 9, 16, 17), ragged lengths with
+    several 128-query blocks, output and LSE against the oracle."""
+    import math
+    import random
+
+    announce(f"varlen groups nseq={nseq} hkv={h_kv}")
+    rng = random.Random(nseq * 10 + h_kv)
+    lens = [rng.choice([0, 1, rng.randint(2, 400)]) for _ in range(nseq)]
+    lens[0] = max(lens[0], 300)
+    h_q, d = 4 * h_kv, 128
+    torch.manual_seed(nseq)
+    qs = [randn(n, h_q, d, dtype=torch.bfloat16) for n in lens]
+    ks = [randn(n, h_kv, d, dtype=torch.bfloat16) for n in lens]
+    vs = [randn(n, h_kv, d, dtype=torch.bfloat16) for n in lens]
+    q, cu, mx = fused_attn.pack_varlen(qs)
+    k, _, _ = fused_attn.pack_varlen(ks)
+    v, _, _ = fused_attn.pack_varlen(vs)
+    out, lse = _hip.varlen_fwd(q, k, v, cu, cu, mx, mx, causal=True, return_lse=True)
+    ref = orc.attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), cu.cpu(), causal=True)
+    assert max_err(out, ref) <= TOL[torch.bfloat16]
+    c = cu.tolist()
+    for i, n in enumerate(lens):
+        if n == 0:
+            continue
+        qf = q[c[i]:c[i + 1]].float().cpu().transpose(0, 1)
+        kf = orc.expand_kv(k[c[i]:c[i + 1]].float().cpu().transpose(0, 1)[None], 4)[0]
+        sc = torch.matmul(qf, kf.transpose(-1, -2)) / math.sqrt(d)
+        sc = sc.masked_fill(~orc.causal_mask(n, n), float("-inf"))
+        assert (lse.cpu()[:, c[i]:c[i + 1]] - torch.logsumexp(sc, dim=-1)).abs().max().item() < 2.0 ** -8
+
+
 def test_attention_triton_alias_gives_the_kernel_result():
     from fused_attn.triton_fwd import attention_triton, attention_varlen_triton
 
