@@ -60,9 +60,9 @@ def test_fp8_decode_is_exact_for_every_code(dtype):
     assert torch.equal(out, want)
 
 
-def test_baseline_fp8_decode_config():
+def test_benchmark_fp8_decode_workload():
     """B=16, Hq=64, Hkv=8, n_q=1, n_k=65536, D=128; K/V N(0,1) fp32 quantised per 64-key block."""
-    announce("baseline fp8 decode")
+    announce("benchmark fp8 decode")
     gen = torch.Generator(device="cuda").manual_seed(0)
     q = randn(16, 64, 1, 128, dtype=torch.bfloat16, gen=gen)
     k8, ks = fused_attn.quantize_kv_fp8(randn(16, 8, 65536, 128, gen=gen))

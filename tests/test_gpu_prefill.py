@@ -126,7 +126,7 @@ def test_unsupported_head_dim_raises_loudly():
         _hip.fwd(q, q, q)
 
 
-# ---- BASELINE-sized workloads ------------------------------------------------------------------
+# ---- benchmark-sized workloads ------------------------------------------------------------------
 
 
 @pytest.mark.parametrize("cfg", [
@@ -134,9 +134,9 @@ def test_unsupported_head_dim_raises_loudly():
     dict(b=4, hq=16, hkv=16, n=4096, d=64, layout="bhnd"),
     dict(b=4, hq=32, hkv=8, n=4096, d=128, layout="bnhd"),
 ])
-def test_baseline_prefill_configs(cfg):
+def test_benchmark_prefill_workloads(cfg):
     """Causal bf16 prefill at the benchmark sizes; oracle in fp32 on the GPU, per (batch, kv group)."""
-    announce(f"baseline prefill {cfg}")
+    announce(f"benchmark prefill {cfg}")
     b, hq, hkv, n, d = cfg["b"], cfg["hq"], cfg["hkv"], cfg["n"], cfg["d"]
     gen = torch.Generator(device="cuda").manual_seed(0)
     if cfg["layout"] == "bnhd":

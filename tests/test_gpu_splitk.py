@@ -1,5 +1,5 @@
 """Split-K flash-decoding on the HIP kernels vs the fp32 oracle
-(reference: tests/test_splitk_fp8.py:16-41), plus the BASELINE decode workloads."""
+(reference: tests/test_splitk_fp8.py:16-41), plus the 32k-key benchmark decode workloads."""
 import pytest
 import torch
 
@@ -75,9 +75,9 @@ def test_workspace_too_small_is_an_error():
 
 
 @pytest.mark.parametrize("n_q,causal", [(1, False), (16, True)])
-def test_baseline_decode_configs(n_q, causal):
+def test_benchmark_decode_workloads(n_q, causal):
     """B=32, Hq=32, Hkv=8, n_k=32768, D=128 bf16 with 128-key partitions (and the n_q=16 spec-decode shape)."""
-    announce(f"baseline decode nq={n_q} causal={causal}")
+    announce(f"benchmark decode nq={n_q} causal={causal}")
     gen = torch.Generator(device="cuda").manual_seed(0)
     q = randn(32, 32, n_q, 128, dtype=torch.bfloat16, gen=gen)
     k = randn(32, 8, 32768, 128, dtype=torch.bfloat16, gen=gen)

@@ -1,5 +1,5 @@
 """Packed variable-length prefill on the HIP kernel vs the per-sequence fp32 oracle
-(reference: tests/test_varlen.py:15-43), plus the BASELINE varlen workload and a
+(reference: tests/test_varlen.py:15-43), plus the 16-sequence benchmark workload and a
 sentinel check that no row outside the sequences is written."""
 import pytest
 import torch
@@ -66,9 +66,9 @@ def test_varlen_writes_only_sequence_rows():
     assert max_err(out[:total], ref[:total]) <= TOL[torch.bfloat16]
 
 
-def test_baseline_varlen_config():
+def test_benchmark_varlen_workload():
     """16 sequences, lengths ~U[0, 4096] by seed with one 0 and one 1; Hq=32, Hkv=8, D=128, bf16, causal."""
-    announce("baseline varlen")
+    announce("benchmark varlen")
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(0, 4097, (16,), generator=g).tolist()
     lens[0], lens[1] = 0, 1
