@@ -574,64 +574,69 @@ attn_splitk_kernel(const TileArgs a) {
 // Log-sum-exp merge of split-K partials (triton_splitk.py:99-127), with each partial
 // O_s stored normalised (O_s = un-normalised partial / l_s):
 //   m = max_s m_s;  w_s = 2^(m_s - m) l_s;  O = sum_s w_s O_s / sum_s w_s   (0 when the sum is 0)
-// One 256-thread workgroup per output row; D/4 threads cover a partial row with
-// 8-byte loads (4 elements), so 256/(D/4) splits are read concurrently.
+// One 256-thread workgroup per output row; D/8 threads cover a partial row with 16-byte
+// loads (8 elements), so 256/(D/8) partials are read concurrently.  Each thread merges
+// its partials online (running max, rescaled sums), and the threads' (m, l, acc) triples
+// are merged through LDS at the end: one pass over the partials, no separate max pass.
 template <int D, class E>
 __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c) {
-  constexpr int TPS = D / 4;
+  constexpr int TPS = D / 8;
   constexpr int SPB = 256 / TPS;
   constexpr float NEG_INF = -__builtin_inff();
-  __shared__ float red[256];
-  __shared__ f32x4 part[SPB][TPS];
-  __shared__ float lpart[SPB];
+  __shared__ f32x4 part[SPB][TPS][2];
+  __shared__ f32x2 mlpart[SPB];
 
   const int64_t row = blockIdx.x;  // (b, hq, qi) flattened
   const int S = c.n_split;
   const float* ml = c.ml + row * S * 2;
   const uint16_t* op = c.opart + row * (int64_t)S * D;
   const int tid = (int)threadIdx.x;
-
-  float m = NEG_INF;
-  for (int s = tid; s < S; s += 256) m = fmaxf(m, ml[2 * s]);
-  red[tid] = m;
-  __syncthreads();
-#pragma unroll
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
-    __syncthreads();
-  }
-  const float mx = red[0];
-  const float m_safe = (mx == NEG_INF) ? 0.f : mx;
-
   const int sg = tid / TPS, dq = tid % TPS;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-#pragma unroll 4
+
+  // Online merge of partials sg, sg + SPB, ...: (m, l, acc) with acc and l relative to 2^m.
+  // An empty partial (m_s = -inf, l_s = 0) gets weight 0; m stays -inf until a partial
+  // with keys arrives, and the -inf guards keep 2^(-inf - -inf) out of the sums.
+  float m = NEG_INF, l = 0.f;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
   for (int s = sg; s < S; s += SPB) {
     const f32x2 st = __builtin_bit_cast(f32x2, ld8(ml + 2 * s));
-    const float w = fast_exp2(st[0] - m_safe) * st[1];
-    l += w;
-    const u32x2 pv = ld8(op + (int64_t)s * D + 4 * dq);
-    acc += w * f32x4{lo_f32<E>(pv[0]), hi_f32<E>(pv[0]), lo_f32<E>(pv[1]), hi_f32<E>(pv[1])};
+    const u32x4 pv = ld16(op + (int64_t)s * D + 8 * dq);
+    const float m_new = fmaxf(m, st[0]);
+    const float m_ref = (m_new == NEG_INF) ? 0.f : m_new;
+    const float alpha = fast_exp2(m - m_ref);  // 0 while m = -inf
+    const float w = fast_exp2(st[0] - m_ref) * st[1];
+    l = l * alpha + w;
+    acc0 = acc0 * alpha + w * f32x4{lo_f32<E>(pv[0]), hi_f32<E>(pv[0]), lo_f32<E>(pv[1]), hi_f32<E>(pv[1])};
+    acc1 = acc1 * alpha + w * f32x4{lo_f32<E>(pv[2]), hi_f32<E>(pv[2]), lo_f32<E>(pv[3]), hi_f32<E>(pv[3])};
+    m = m_new;
   }
-  part[sg][dq] = acc;
-  if (dq == 0) lpart[sg] = l;
+  part[sg][dq][0] = acc0;
+  part[sg][dq][1] = acc1;
+  if (dq == 0) mlpart[sg] = f32x2{m, l};
   __syncthreads();
   if (tid < TPS) {
-    f32x4 tot = part[0][tid];
-    float lt = lpart[0];
+    float mx = NEG_INF;
 #pragma unroll
-    for (int k = 1; k < SPB; ++k) {
-      tot += part[k][tid];
-      lt += lpart[k];
+    for (int k = 0; k < SPB; ++k) mx = fmaxf(mx, mlpart[k][0]);
+    const float m_ref = (mx == NEG_INF) ? 0.f : mx;
+    f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
+    float lt = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < SPB; ++k) {
+      const float a = fast_exp2(mlpart[k][0] - m_ref);
+      lt += a * mlpart[k][1];
+      t0 += a * part[k][tid][0];
+      t1 += a * part[k][tid][1];
     }
     const float inv = 1.f / ((lt == 0.f) ? 1.f : lt);
     const int qi = (int)(row % c.nq);
     const int64_t bh = row / c.nq;
     const int hq = (int)(bh % c.hq);
     const int64_t b = bh / c.hq;
-    uint16_t* o = (uint16_t*)c.o + b * c.sob + (int64_t)hq * c.soh + (int64_t)qi * c.son + 4 * tid;
-    st8(o, u32x2{pack2<E>(tot[0] * inv, tot[1] * inv), pack2<E>(tot[2] * inv, tot[3] * inv)});
+    uint16_t* o = (uint16_t*)c.o + b * c.sob + (int64_t)hq * c.soh + (int64_t)qi * c.son + 8 * tid;
+    st8(o, u32x2{pack2<E>(t0[0] * inv, t0[1] * inv), pack2<E>(t0[2] * inv, t0[3] * inv)});
+    st8(o + 4, u32x2{pack2<E>(t1[0] * inv, t1[1] * inv), pack2<E>(t1[2] * inv, t1[3] * inv)});
   }
 }
 
