@@ -687,12 +687,18 @@ TileArgs common_args(const fa_fwd_params& p) {
 
 int splitk_waves_for_rows(int rows) { return rows <= 32 ? 1 : (rows <= 64 ? 2 : 4); }
 
-// Partitions per workgroup.  One partition per workgroup measured fastest on MI355X
-// for 16-bit and FP8 caches (fine-grained workgroups keep every CU's memory pipeline
-// full to the end of the grid); several per workgroup only cap the grid at kMaxWgs.
-int splitk_parts_per_wg(int64_t items, int n_split) {
-  constexpr int64_t kMaxWgs = int64_t{1} << 20;
-  const int64_t want = (items * n_split + kMaxWgs - 1) / kMaxWgs;
+// Partitions per workgroup.  One partition per workgroup measured fastest on MI355X for
+// one-wave 16-bit decode (fine-grained workgroups keep every CU's memory pipeline full to
+// the end of the grid; two per workgroup: -3% at 128-key partitions).  Workgroups with
+// less memory work per instruction stream (FP8 tiles, or row blocks of 2-4 waves) gain
+// 2-2.4% from two partitions when the grid is fine (at least 16384 workgroups, 64 per CU);
+// coarser grids keep one so that every CU stays busy.  Beyond that, several partitions per
+// workgroup only cap the grid at kMaxWgs.  Paged decode keeps one (a workgroup's pages
+// must fit the block-table entries it holds).
+int splitk_parts_per_wg(int64_t items, int n_split, bool fp8, int nw, bool paged) {
+  constexpr int64_t kMaxWgs = int64_t{1} << 20, kFineGrid = int64_t{1} << 14;
+  int64_t want = (items * n_split + kMaxWgs - 1) / kMaxWgs;
+  if (!paged && (fp8 || nw > 1) && items * n_split >= kFineGrid) want = std::max<int64_t>(want, 2);
   return (int)std::max<int64_t>(1, std::min<int64_t>(want, n_split));
 }
 
@@ -743,7 +749,7 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
   a.n_split = S;
   a.split_len = split_len;
   const int64_t items = (int64_t)p.batch * p.heads_kv * a.n_rowblk;
-  a.ppw = splitk_parts_per_wg(items, S);
+  a.ppw = splitk_parts_per_wg(items, S, p.kv_dtype == FA_DTYPE_FP8_E4M3, nw, kv != nullptr);
   a.n_chunk = (S + a.ppw - 1) / a.ppw;
   if (kv != nullptr) {
     // a workgroup's keys span at most (ppw * split_len - 1) / page_size + 2 pages, and it

@@ -5,7 +5,7 @@ import torch
 
 import fused_attn
 from fused_attn import _hip, ops
-from helpers import TOL, announce, max_err, randn
+from helpers import FP8_TOL, TOL, announce, max_err, randn
 from oracle import attention_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -72,6 +72,30 @@ def test_workspace_too_small_is_an_error():
     assert need == 1 * 4 * 1 * 4 * (64 * 2 + 8)  # 16-bit partials + fp32 (max, sum) pairs
     out = _hip.splitk(q, k, k, split_len=128, workspace=ws)  # too small -> the wrapper allocates its own
     assert max_err(out, orc.attention(q.cpu(), k.cpu(), k.cpu())) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_two_partitions_per_workgroup_with_an_odd_count(fp8):
+    """Fine grids of multi-wave row blocks (and FP8 caches) run two partitions per workgroup:
+    257 partitions leave the last workgroup one, causal spec-decode rows span two waves."""
+    announce(f"two partitions per workgroup fp8={fp8}")
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    n_k = 128 * 257 - 50
+    q = randn(8, 32, 16, 128, dtype=torch.bfloat16, gen=gen)
+    if fp8:
+        k8, ks = fused_attn.quantize_kv_fp8(randn(8, 8, n_k, 128, gen=gen))
+        v8, vs = fused_attn.quantize_kv_fp8(randn(8, 8, n_k, 128, gen=gen))
+        out = fused_attn.attention_fp8(q, k8, ks, v8, vs, causal=True, split_len=128)
+        ref = torch.empty(q.shape, device="cuda")
+        for bi in range(8):
+            ref[bi:bi + 1] = orc.attention_fp8(q[bi:bi + 1], k8[bi:bi + 1], ks[bi:bi + 1], v8[bi:bi + 1],
+                                               vs[bi:bi + 1], causal=True)
+        assert max_err(out, ref) <= FP8_TOL
+    else:
+        k = randn(8, 8, n_k, 128, dtype=torch.bfloat16, gen=gen)
+        v = randn(8, 8, n_k, 128, dtype=torch.bfloat16, gen=gen)
+        out = fused_attn.attention_splitk(q, k, v, causal=True, split_len=128)
+        assert max_err(out, orc.attention_chunked(q, k, v, causal=True)) <= TOL[torch.bfloat16]
 
 
 @pytest.mark.parametrize("n_q,causal", [(1, False), (16, True)])
