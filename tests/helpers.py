@@ -12,6 +12,17 @@ def max_err(out: torch.Tensor, ref: torch.Tensor) -> float:
     return (out.float() - ref.float().to(out.device)).abs().max().item() if out.numel() else 0.0
 
 
+def close(out: torch.Tensor, ref: torch.Tensor, tol: float) -> bool:
+    """The reference's bar, torch.testing.assert_close(atol=tol, rtol=tol) (tests/test_correctness.py:84-85,
+    tests/test_splitk_fp8.py:29): |out - ref| <= tol + tol * |ref| everywhere.  max_err <= tol (used by
+    the fixed-case tests) is stricter; with large softmax scales the output follows single V rows of
+    magnitude ~4, where one bf16 ulp (0.031) already exceeds an absolute 2e-2."""
+    if not out.numel():
+        return True
+    r = ref.float().to(out.device)
+    return bool(((out.float() - r).abs() <= tol + tol * r.abs()).all().item())
+
+
 def announce(msg: str) -> None:
     """Name the case before GPU work starts, flushed, so a crash still identifies it."""
     print(f"[case] {msg}", flush=True)

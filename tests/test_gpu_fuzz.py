@@ -4,7 +4,8 @@ Complements the fixed matrices of the other GPU tests (which follow the referenc
 tests/test_correctness.py, test_varlen.py and test_splitk_fp8.py) with shapes no one
 picked by hand: ragged lengths, every GQA ratio that divides the heads, both layouts,
 custom and negative scales.  Each case is drawn from its own seed and named before
-it runs."""
+it runs.  The bar is the reference's assert_close(atol=tol, rtol=tol), since large
+random scales produce outputs of magnitude ~4 (see helpers.close)."""
 import math
 import random
 
@@ -13,7 +14,7 @@ import torch
 
 import fused_attn
 from fused_attn.triton_fwd import attention_triton
-from helpers import FP8_TOL, TOL, announce, max_err, randn
+from helpers import FP8_TOL, TOL, announce, close, max_err, randn
 from oracle import attention_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -54,7 +55,7 @@ def test_fuzz_dense(seed):
     out = fused_attn.attention(q, k, v, causal=causal, scale=scale)
     ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal, scale=scale)
     assert out.shape == q.shape and out.dtype == dtype
-    assert max_err(out, ref) <= _tol(dtype)
+    assert close(out, ref, _tol(dtype)), max_err(out, ref)
 
 
 @pytest.mark.parametrize("seed", range(32))
@@ -77,7 +78,7 @@ def test_fuzz_splitk(seed):
     v = randn(b, hkv, n_k, d, dtype=dtype)
     out = fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split_len)
     ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal)
-    assert max_err(out, ref) <= TOL[dtype]
+    assert close(out, ref, TOL[dtype]), max_err(out, ref)
 
 
 @pytest.mark.parametrize("seed", range(16))
@@ -97,7 +98,7 @@ def test_fuzz_fp8_splitk(seed):
     v8, vs = fused_attn.quantize_kv_fp8(randn(b, hkv, n_k, d))
     out = fused_attn.attention_fp8(q, k8, ks, v8, vs, split_len=split_len)
     ref = orc.attention_fp8(q.cpu(), k8.cpu(), ks.cpu(), v8.cpu(), vs.cpu())
-    assert max_err(out, ref) <= FP8_TOL
+    assert close(out, ref, FP8_TOL), max_err(out, ref)
 
 
 @pytest.mark.parametrize("seed", range(24))
@@ -123,7 +124,7 @@ def test_fuzz_varlen(seed):
     out = fused_attn.attention_varlen(q, k, v, cu_q, cu_k, max_q, max_k, causal=causal)
     ref = orc.attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=causal)
     assert out.shape == q.shape
-    assert max_err(out, ref) <= _tol(dtype)
+    assert close(out, ref, _tol(dtype)), max_err(out, ref)
 
 
 @pytest.mark.parametrize("seed", range(16))
@@ -150,7 +151,7 @@ def test_fuzz_paged(seed):
                                                  generator=torch.Generator().manual_seed(seed))
     out = fused_attn.attention_paged(q, kc, vc, bt, sl, causal=causal, split_len=split_len)
     ref = orc.attention_paged(q, kc, vc, bt, sl, causal=causal)
-    assert max_err(out, ref) <= TOL[dtype]
+    assert close(out, ref, TOL[dtype]), max_err(out, ref)
 
 
 def test_fuzz_lse_matches_logsumexp():
