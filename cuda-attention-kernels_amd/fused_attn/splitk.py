@@ -46,8 +46,9 @@ def attention_splitk(
 
     ``num_splits`` is honoured as in the reference: each partition gets
     ``ceil(ceil(n_k / num_splits) / 64) * 64`` keys.  ``split_len`` (a multiple
-    of 64) sets the partition size directly.  With neither, partitions hold 128
-    keys.  CPU tensors use the unfused reference.
+    of 64) sets the partition size directly.  With neither, ``ops.default_split_len``
+    chooses it (partitions as long as possible while the grid keeps about
+    SPLITK_TARGET_WGS workgroups).  CPU tensors use the unfused reference.
     """
     d = q.shape[-1]
     n_k = k.shape[-2]

@@ -180,3 +180,18 @@ def test_head_dim_256_views_varlen_and_decode_shapes(dtype):
     ref = orc.attention(q.cpu(), k.cpu(), v.cpu())
     assert max_err(out, ref) <= TOL[dtype]
     assert max_err(_hip.fwd(q, k, v), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_long_context_prefill(causal):
+    """N=16384 (128 query blocks per head, 256 key tiles): grid, schedule and tail at long context."""
+    announce(f"long-context prefill causal={causal}")
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    q = randn(1, 8, 16384, 128, dtype=torch.bfloat16, gen=gen)
+    k = randn(1, 2, 16384, 128, dtype=torch.bfloat16, gen=gen)
+    v = randn(1, 2, 16384, 128, dtype=torch.bfloat16, gen=gen)
+    out = fused_attn.attention(q, k, v, causal=causal)
+    ref = orc.attention_chunked(q, k, v, causal=causal, heads_per_chunk=1, rows_per_chunk=2048)
+    err = max_err(out, ref)
+    print(f"max_abs_err={err:.3e}", flush=True)
+    assert err <= TOL[torch.bfloat16]

@@ -134,3 +134,18 @@ def test_benchmark_decode_workloads(n_q, causal):
     op_out = fused_attn.attention(q, k, v, causal=causal)
     assert torch.equal(op_out, fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split))
     assert max_err(op_out, ref) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("split_len", [128, None])
+def test_long_context_decode(split_len):
+    """262144 keys: 2048 partitions per (batch, kv-head) at 128-key partitions, and the default policy."""
+    announce(f"long-context decode split={split_len}")
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    q = randn(2, 32, 1, 128, dtype=torch.bfloat16, gen=gen)
+    k = randn(2, 8, 262144, 128, dtype=torch.bfloat16, gen=gen)
+    v = randn(2, 8, 262144, 128, dtype=torch.bfloat16, gen=gen)
+    out = fused_attn.attention_splitk(q, k, v, split_len=split_len)
+    ref = orc.attention_chunked(q, k, v, heads_per_chunk=4)
+    err = max_err(out, ref)
+    print(f"max_abs_err={err:.3e}", flush=True)
+    assert err <= TOL[torch.bfloat16]
