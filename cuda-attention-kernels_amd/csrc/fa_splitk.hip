@@ -31,6 +31,10 @@
 // K/V go global -> LDS by DMA (buffer_load ... lds) in their storage type; FP8 K/V
 // stay 8-bit in LDS (half the LDS per stage, so more workgroups per CU) and are
 // widened to 16 bits when read as MFMA operands, V through ds_read_b64_tr_b8.
+// LDS holds two stages (tile t+1 loads while tile t is read), or, for one-wave
+// workgroups where LDS rather than registers bounds the workgroups per CU, a single
+// stage whose K and V halves are refilled as soon as they have been read (the choice
+// is made per launch in launch_split_nw).
 //
 // Paged K/V (PAGED): each sequence's keys live in pages of a shared pool, found
 // through its block-table row, and each sequence has its own length.  A workgroup
