@@ -102,6 +102,32 @@ def test_null_params(lib):
     assert lib.fa_attention_splitk(None, 128, None, 0, None) == _hip.FA_ERR_INVALID_ARGUMENT
 
 
+def test_last_error_is_per_thread(lib):
+    """fa_last_error() is thread-local: two threads that fail differently, in interleaved order, each
+    read their own message (ctypes releases the GIL around the calls)."""
+    import threading
+
+    start = threading.Barrier(2)
+    failed = threading.Barrier(2)
+    seen = {}
+
+    def worker(name, over, msg):
+        p = _params(**over)
+        start.wait()
+        rc = lib.fa_attention_fwd(ctypes.byref(p), None)
+        failed.wait()  # both threads have failed before either reads its message
+        seen[name] = (rc, lib.fa_last_error().decode(), msg)
+
+    threads = [threading.Thread(target=worker, args=("a", dict(head_dim=96), "head_dim")),
+               threading.Thread(target=worker, args=("b", dict(q=0x10002), "aligned"))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for name, (rc, text, msg) in seen.items():
+        assert rc != _hip.FA_OK and msg in text, (name, text)
+
+
 def test_empty_requests_succeed_without_launch(lib):
     assert lib.fa_attention_fwd(ctypes.byref(_params(batch=0)), None) == _hip.FA_OK
     assert lib.fa_attention_fwd(ctypes.byref(_params(seqlen_q=0)), None) == _hip.FA_OK

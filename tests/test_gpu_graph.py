@@ -67,6 +67,17 @@ def test_graph_prefill():
     _capture_and_replay(fn, [q, k, v], fn)
 
 
+def test_graph_varlen_prefill():
+    announce("graph varlen prefill")
+    lens = [300, 0, 1, 129, 77]  # 5 sequences x 2 kv-heads: the grid is padded to 16 groups
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    q, cu, mx = fused_attn.pack_varlen([randn(n, 8, 128, dtype=torch.bfloat16, gen=gen) for n in lens])
+    k, _, _ = fused_attn.pack_varlen([randn(n, 2, 128, dtype=torch.bfloat16, gen=gen) for n in lens])
+    v, _, _ = fused_attn.pack_varlen([randn(n, 2, 128, dtype=torch.bfloat16, gen=gen) for n in lens])
+    fn = lambda: fused_attn.attention_varlen(q, k, v, cu, cu, mx, mx, causal=True)  # noqa: E731
+    _capture_and_replay(fn, [q, k, v], fn)
+
+
 def test_graph_paged_decode():
     announce("graph paged decode")
     gen = torch.Generator(device="cuda").manual_seed(0)
