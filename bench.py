@@ -381,7 +381,7 @@ def main():
                    "seq_len": c["n"], "head_dim": c["d"], "causal": True, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": _traffic_bytes(), "kernel": "attn_fwd_kernel<128,BF16>",
+                     "traffic": _traffic_bytes(), "kernel": "attn_fwd_kernel<128,BF16,8>",
                      "kernel_ms": round(ev * 1e3, 4)},
     }
     line["prefill_other"] = bench_prefill_extras(max(5, a.steps // 2), max(2, a.warmup))
