@@ -195,3 +195,19 @@ def test_long_context_prefill(causal):
     err = max_err(out, ref)
     print(f"max_abs_err={err:.3e}", flush=True)
     assert err <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("n_q,n_k,causal", [(4200, 5000, True), (4096, 3000, True), (4100, 4100, False),
+                                            (5000, 4200, True)])
+def test_eight_wave_blocks_ragged_and_offset(n_q, n_k, causal):
+    """Dense D=128 with >= 4096 queries runs 256-query workgroups: a partial last block, bottom-right
+    causal offsets both ways (rows that see no key when n_k < n_q) and the per-wave causal skip."""
+    announce(f"8-wave prefill nq={n_q} nk={n_k} causal={causal}")
+    gen = torch.Generator(device="cuda").manual_seed(n_q + n_k)
+    q = randn(1, 8, n_q, 128, dtype=torch.bfloat16, gen=gen)
+    k = randn(1, 2, n_k, 128, dtype=torch.bfloat16, gen=gen)
+    v = randn(1, 2, n_k, 128, dtype=torch.bfloat16, gen=gen)
+    out = fused_attn.attention(q, k, v, causal=causal)
+    ref = orc.attention_chunked(q, k, v, causal=causal, heads_per_chunk=2, rows_per_chunk=1024)
+    assert not torch.isnan(out).any()
+    assert max_err(out, ref) <= TOL[torch.bfloat16]
