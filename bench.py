@@ -340,7 +340,7 @@ def run_only(which, steps, warmup):
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
