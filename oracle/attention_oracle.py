@@ -39,6 +39,10 @@ How each function is pinned (checked in tests/test_oracle.py):
   attention_paged      vs dense attention on the K/V that were scattered into randomly
                        ordered pages (ragged lengths, zero-length sequences, causal), and a
                        page index outside the pool contributes zero keys.
+
+tests/test_oracle_mutants.py plants plausible mistakes in copies of this module (mask offsets,
+dropped scale, swapped operands, wrong head mapping, rounding rules, constants, combine terms)
+and checks that the pins above fail on each of them.
 """
 from __future__ import annotations
 
