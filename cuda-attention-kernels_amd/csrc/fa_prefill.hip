@@ -2,11 +2,11 @@
 //
 // Serves the reference's dense and varlen prefill, attn_fwd_mma_kernel
 // (csrc/flash_attn_mma.cu:63-242) and _attn_fwd_kernel
-// (fused_attn/triton_fwd.py:85-172), for 16-bit Q/K/V with D in {64, 128, 256}.
+// (fused_attn/triton_fwd.py:85-172), for 16-bit Q/K/V with D in {32, 64, 128, 256}.
 //
 // A workgroup of NW waves (8 for dense D=128, otherwise 4) covers NW*32 queries of one
-// q-head; wave w owns 32 of them.  K and V stream through LDS in 64-key tiles (128 at D=64,
-// 32 at D=256), each in two buffers filled
+// q-head; wave w owns 32 of them.  K and V stream through LDS in 64-key tiles (128 at D=64
+// and D=32, 32 at D=256), each in two buffers filled
 // straight from memory (buffer_load ... lds).  The product order per wave is the
 // same as in the split-K kernel (S^T = K Q^T with the softmax lane-local,
 // P^T kept in VGPRs as the B operand of O^T += V^T P^T), but the loop is
@@ -41,10 +41,11 @@ template <int D, class E, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 attn_fwd_kernel(const TileArgs a) {
   // 64-key tiles at D=128, 128-key tiles at D=64, 32-key tiles at D=256: 16 KiB per K (or V)
-  // tile and 32 MFMAs per iteration in every case (measured: D=64 prefill 3% faster than with
-  // 64-key tiles).  At D=256 the fp32 output accumulator alone takes 128 registers per lane,
-  // so the kernel runs one wave per SIMD there.
-  constexpr int BN = D == 64 ? 128 : (D == 256 ? 32 : 64);
+  // tile and 32 MFMAs per iteration (measured: D=64 prefill 3% faster than with 64-key
+  // tiles).  D=32 keeps 128-key tiles (8 KiB, 16 MFMAs per iteration): the scores of a tile
+  // already take 64 registers per lane.  At D=256 the fp32 output accumulator alone takes
+  // 128 registers per lane, so the kernel runs one wave per SIMD there.
+  constexpr int BN = (D == 64 || D == 32) ? 128 : (D == 256 ? 32 : 64);
   static_assert(NW == 4 || (NW == 8 && D != 256), "4 or 8 waves (two per SIMD) per workgroup");
   using Shape = TileShape<D, BN>;
   constexpr int TILE = Shape::TILE;
@@ -52,7 +53,7 @@ attn_fwd_kernel(const TileArgs a) {
   constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
   constexpr int DB = D / 32;   // 32-wide d blocks of O^T
   constexpr int QPW = (TILE * 2 / 1024) / NW;  // 1-KiB DMA blocks per wave per K (or V) tile
-  static_assert(D == 64 || D == 128 || D == 256, "head dim");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dim");
   static_assert((TILE * 2) % (1024 * NW) == 0, "direct loads must split evenly over the waves");
   constexpr float NEG_INF = -__builtin_inff();
 
@@ -459,7 +460,7 @@ static hipError_t launch_fwd(const TileArgs& a, hipStream_t stream) {
 
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
   const bool mfma = (p.dtype == FA_DTYPE_BF16 || p.dtype == FA_DTYPE_F16) &&
-                    (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256);
+                    (p.head_dim == 32 || p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256);
   if (!mfma) return run_fwd_generic(p, varlen, stream, err);
   TileArgs a = common_args(p);
   a.o = p.o;
@@ -508,6 +509,8 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
     }
   } else if (p.head_dim == 64) {
     e = bf ? launch_fwd<64, BF16, 4>(a, stream) : launch_fwd<64, F16, 4>(a, stream);
+  } else if (p.head_dim == 32) {
+    e = bf ? launch_fwd<32, BF16, 4>(a, stream) : launch_fwd<32, F16, 4>(a, stream);
   } else if (p.head_dim == 256) {
     e = bf ? launch_fwd<256, BF16, 4>(a, stream) : launch_fwd<256, F16, 4>(a, stream);
   }

@@ -11,7 +11,8 @@ namespace fa {
 // can fill a tile.  Physical chunk = logical chunk ^ swizzle(row).
 //
 // A chunk's bank group (16 bytes = 4 of the 64 banks) is its physical index mod 16,
-// since rows are multiples of 256 bytes at D >= 128.  At D = 256 a row is two bank
+// since rows are multiples of 256 bytes at D >= 128; at D = 64 and 32 a 256-byte line holds
+// 2 and 4 rows.  At D = 256 a row is two bank
 // lines; the XOR values stay below 16, so they keep a chunk's high bit and give the
 // same bank pattern as at D = 128.
 template <int D, int BN>
@@ -23,9 +24,10 @@ struct TileShape {
   // K rows are read 16 at a time at one logical chunk: map them to 16 distinct bank groups.
   __device__ static constexpr int swz_k(int row) { return (row / ROWS_PER_256B) % (CPR < 16 ? CPR : 16); }
   // V is read transposed: 4 consecutive rows (starting at a multiple of 4) x 4 chunks
-  // (starting at a multiple of 4) per 32 lanes.
+  // (starting at a multiple of 4) per 32 lanes.  At D = 32 those are 4 whole 64-byte rows,
+  // one 256-byte bank line, so no swizzle is needed.
   __device__ static constexpr int swz_v(int row) {
-    return D >= 128 ? 4 * (row & 3) + ((row >> 2) & 3) : 4 * ((row >> 1) & 1);
+    return D >= 128 ? 4 * (row & 3) + ((row >> 2) & 3) : (D == 64 ? 4 * ((row >> 1) & 1) : 0);
   }
 };
 

@@ -77,8 +77,8 @@ SPLITK_HEAD_DIMS = (64, 128, 256)
 def _hip_kernel_for(q: torch.Tensor, k: torch.Tensor) -> str:
     """Which HIP kernel family serves this call: ``splitk`` or ``fwd``.
 
-    fp32 and head dims other than 64 / 128 always take ``fwd``, whose generic kernel
-    covers them (the reference's Triton path likewise served every shape).
+    fp32 and head dims other than 64 / 128 / 256 always take ``fwd``, whose MFMA or generic
+    kernel covers them (the reference's Triton path likewise served every shape).
     """
     if q.dtype not in SPLITK_DTYPES or q.shape[-1] not in SPLITK_HEAD_DIMS:
         return "fwd"
