@@ -107,7 +107,7 @@ def bench_prefill(steps, warmup):
 
 
 def bench_prefill_extras(steps, warmup):
-    """The other prefill configurations (D=64 MHA, the [B,N,H,D] view, the 16-sequence varlen batch), and D=32 and 256."""
+    """The other prefill configurations (D=64 MHA, the [B,N,H,D] view, the 16-sequence varlen batch), and D=16, 32 and 256."""
     import torch
 
     import fused_attn
@@ -133,6 +133,9 @@ def bench_prefill_extras(steps, warmup):
     v = torch.randn(4, 16, 4096, 32, device="cuda", generator=g).bfloat16()
     entry("prefill_d32_mha", "causal MHA prefill B=4 Hq=Hkv=16 N=4096 D=32 bf16",
           lambda: fused_attn.attention(q, k, v, causal=True), attn_flops(4, 16, 4096, 32, True))
+    q, k, v = (x[..., :16].contiguous() for x in (q, k, v))
+    entry("prefill_d16_mha", "causal MHA prefill B=4 Hq=Hkv=16 N=4096 D=16 bf16",
+          lambda: fused_attn.attention(q, k, v, causal=True), attn_flops(4, 16, 4096, 16, True))
     q = torch.randn(2, 16, 4096, 256, device="cuda", generator=g).bfloat16()
     k = torch.randn(2, 4, 4096, 256, device="cuda", generator=g).bfloat16()
     v = torch.randn(2, 4, 4096, 256, device="cuda", generator=g).bfloat16()

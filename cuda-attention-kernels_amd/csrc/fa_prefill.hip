@@ -2,11 +2,11 @@
 //
 // Serves the reference's dense and varlen prefill, attn_fwd_mma_kernel
 // (csrc/flash_attn_mma.cu:63-242) and _attn_fwd_kernel
-// (fused_attn/triton_fwd.py:85-172), for 16-bit Q/K/V with D in {32, 64, 128, 256}.
+// (fused_attn/triton_fwd.py:85-172), for 16-bit Q/K/V with D in {16, 32, 64, 128, 256}.
 //
 // A workgroup of NW waves (8 for dense D=128, otherwise 4) covers NW*32 queries of one
-// q-head; wave w owns 32 of them.  K and V stream through LDS in 64-key tiles (128 at D=64
-// and D=32, 32 at D=256), each in two buffers filled
+// q-head; wave w owns 32 of them.  K and V stream through LDS in 64-key tiles (128 at D <= 64,
+// 32 at D=256), each in two buffers filled
 // straight from memory (buffer_load ... lds).  The product order per wave is the
 // same as in the split-K kernel (S^T = K Q^T with the softmax lane-local,
 // P^T kept in VGPRs as the B operand of O^T += V^T P^T), but the loop is
@@ -42,27 +42,34 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D 
 attn_fwd_kernel(const TileArgs a) {
   // 64-key tiles at D=128, 128-key tiles at D=64, 32-key tiles at D=256: 16 KiB per K (or V)
   // tile and 32 MFMAs per iteration (measured: D=64 prefill 3% faster than with 64-key
-  // tiles).  D=32 keeps 128-key tiles (8 KiB, 16 MFMAs per iteration): the scores of a tile
-  // already take 64 registers per lane.  At D=256 the fp32 output accumulator alone takes
-  // 128 registers per lane, so the kernel runs one wave per SIMD there.
-  constexpr int BN = (D == 64 || D == 32) ? 128 : (D == 256 ? 32 : 64);
+  // tiles).  D=32 and D=16 keep 128-key tiles: the scores of a tile already take 64 registers
+  // per lane.  At D=256 the fp32 output accumulator alone takes 128 registers per lane, so the
+  // kernel runs one wave per SIMD there.
+  constexpr int BN = D <= 64 ? 128 : (D == 256 ? 32 : 64);
   static_assert(NW == 4 || (NW == 8 && D != 256), "4 or 8 waves (two per SIMD) per workgroup");
-  using Shape = TileShape<D, BN>;
-  constexpr int TILE = Shape::TILE;
+  // V tiles are at least 32 columns wide, since O^T += V^T P^T works in 32-wide d blocks.  At
+  // D=16 the upper 16 columns of a V row in LDS repeat the lower ones (the DMA reads each source
+  // chunk twice); they feed only O^T rows 16..31, which are never stored.
+  constexpr int DV = D < 32 ? 32 : D;
+  using Shape = TileShape<D, BN>;    // K tiles
+  using VShape = TileShape<DV, BN>;  // V tiles
+  constexpr int TILE = Shape::TILE, VTILE = VShape::TILE;
   constexpr int KB = BN / 32;  // 32-key MFMA blocks per tile
   constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
-  constexpr int DB = D / 32;   // 32-wide d blocks of O^T
-  constexpr int QPW = (TILE * 2 / 1024) / NW;  // 1-KiB DMA blocks per wave per K (or V) tile
-  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dim");
-  static_assert((TILE * 2) % (1024 * NW) == 0, "direct loads must split evenly over the waves");
+  constexpr int DB = DV / 32;  // 32-wide d blocks of O^T
+  constexpr int QPW = (TILE * 2 / 1024) / NW;    // 1-KiB DMA blocks per wave per K tile
+  constexpr int VQPW = (VTILE * 2 / 1024) / NW;  // and per V tile
+  static_assert(D == 16 || D == 32 || D == 64 || D == 128 || D == 256, "head dim");
+  static_assert((TILE * 2) % (1024 * NW) == 0 && (VTILE * 2) % (1024 * NW) == 0,
+                "direct loads must split evenly over the waves");
   constexpr float NEG_INF = -__builtin_inff();
 
   // Four separate arrays: every access names its buffer at compile time, so the
   // compiler can tell that a DMA into one buffer never aliases reads of another.
   __shared__ __align__(16) uint16_t k_buf0[TILE];
   __shared__ __align__(16) uint16_t k_buf1[TILE];
-  __shared__ __align__(16) uint16_t v_buf0[TILE];
-  __shared__ __align__(16) uint16_t v_buf1[TILE];
+  __shared__ __align__(16) uint16_t v_buf0[VTILE];
+  __shared__ __align__(16) uint16_t v_buf1[VTILE];
 
   // ---- work item: (batch, q-head, 128-query block) -----------------------------------
   // Scheduling units: the q-heads of as many kv-heads as keep about kL2UnitBytes of
@@ -191,10 +198,12 @@ attn_fwd_kernel(const TileArgs a) {
     lds_dma16<false>(rk, (uint8_t*)dst + blk * 1024, kperm(r) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16));
   };
   auto dma_v = [&](const __amdgpu_buffer_rsrc_t& rv, uint16_t* dst, int i) __attribute__((always_inline)) {
-    const int blk = wave * QPW + i;
+    const int blk = wave * VQPW + i;
     const int byte = blk * 1024 + lane * 16;
-    const int r = byte / (D * 2), p = (byte % (D * 2)) / 16;
-    lds_dma16<false>(rv, (uint8_t*)dst + blk * 1024, r * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16));
+    const int r = byte / (DV * 2), p = (byte % (DV * 2)) / 16;
+    int c = p ^ VShape::swz_v(r);
+    if constexpr (DV != D) c %= D / 8;  // D=16: the padding chunks re-read their row's chunks
+    lds_dma16<false>(rv, (uint8_t*)dst + blk * 1024, r * (int)vrow_bytes + c * 16);
   };
   auto load_k = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rk = k_rsrc(n0);
@@ -204,7 +213,7 @@ attn_fwd_kernel(const TileArgs a) {
   auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rv = v_rsrc(n0);
 #pragma unroll
-    for (int i = 0; i < QPW; ++i) dma_v(rv, dst, i);
+    for (int i = 0; i < VQPW; ++i) dma_v(rv, dst, i);
   };
 
   // Per-lane LDS element offsets of the MFMA operand reads.
@@ -222,7 +231,7 @@ attn_fwd_kernel(const TileArgs a) {
     for (int hi = 0; hi < 2; ++hi) {
       const int vr_row = 8 * g + 4 * hi + (tr_i >> 2);
       const int col = 32 * d + 16 * tr_dh + 4 * (tr_i & 3);
-      voffs[d][hi] = vr_row * D + (((col >> 3) ^ Shape::swz_v(vr_row)) * 8) + (col & 7);
+      voffs[d][hi] = vr_row * DV + (((col >> 3) ^ VShape::swz_v(vr_row)) * 8) + (col & 7);
     }
   }
 
@@ -295,7 +304,7 @@ attn_fwd_kernel(const TileArgs a) {
     constexpr int NMAX = KB * 8;         // max3 steps for S_{t+1}
     // exp step u runs in S slot u * NQK / NEXP: several per slot, or one every few slots
     static_assert(NEXP % NQK == 0 || NQK % NEXP == 0, "exp steps must spread evenly over the S slots");
-    constexpr int NDMA = 2 * QPW, DMA_EVERY = NM / NDMA;
+    constexpr int NDMA = QPW + VQPW, DMA_EVERY = NM / NDMA;
     static_assert(NM % NDMA == 0, "DMA instructions must spread evenly over the slots");
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) nxt[kb] = f32x16{};
@@ -311,7 +320,7 @@ attn_fwd_kernel(const TileArgs a) {
         opnd[m % (PD + 1)] = ld16(Kn + kb * 32 * D + koffs[s]);
       } else {
         const int i = m - NQK, kb = i / (2 * DB), h = (i / DB) % 2, d = i % DB;
-        const uint16_t* vp = Vc + (kb * 32 + 16 * h) * D;
+        const uint16_t* vp = Vc + (kb * 32 + 16 * h) * DV;
         const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
         const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
         opnd[m % (PD + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
@@ -419,7 +428,7 @@ attn_fwd_kernel(const TileArgs a) {
 #pragma unroll
       for (int i = 0; i < QPW; ++i) dma_k(rk, k_this, i);
 #pragma unroll
-      for (int i = 0; i < QPW; ++i) dma_v(rv, v_next, i);
+      for (int i = 0; i < VQPW; ++i) dma_v(rv, v_next, i);
     }
     lds_dma_wait();
     __syncthreads();
@@ -441,6 +450,7 @@ attn_fwd_kernel(const TileArgs a) {
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
+      if (d * 32 + 8 * rq >= D) continue;  // D=16: O^T rows 16..31 are padding
       const int d0 = d * 32 + 8 * rq + 4 * g;
       st8(op + d0, u32x2{pack2<E>(oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv),
                          pack2<E>(oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv)});
@@ -460,7 +470,8 @@ static hipError_t launch_fwd(const TileArgs& a, hipStream_t stream) {
 
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
   const bool mfma = (p.dtype == FA_DTYPE_BF16 || p.dtype == FA_DTYPE_F16) &&
-                    (p.head_dim == 32 || p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256);
+                    (p.head_dim == 16 || p.head_dim == 32 || p.head_dim == 64 || p.head_dim == 128 ||
+                     p.head_dim == 256);
   if (!mfma) return run_fwd_generic(p, varlen, stream, err);
   TileArgs a = common_args(p);
   a.o = p.o;
@@ -511,6 +522,8 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
     e = bf ? launch_fwd<64, BF16, 4>(a, stream) : launch_fwd<64, F16, 4>(a, stream);
   } else if (p.head_dim == 32) {
     e = bf ? launch_fwd<32, BF16, 4>(a, stream) : launch_fwd<32, F16, 4>(a, stream);
+  } else if (p.head_dim == 16) {
+    e = bf ? launch_fwd<16, BF16, 4>(a, stream) : launch_fwd<16, F16, 4>(a, stream);
   } else if (p.head_dim == 256) {
     e = bf ? launch_fwd<256, BF16, 4>(a, stream) : launch_fwd<256, F16, 4>(a, stream);
   }

@@ -11,8 +11,8 @@ namespace fa {
 // can fill a tile.  Physical chunk = logical chunk ^ swizzle(row).
 //
 // A chunk's bank group (16 bytes = 4 of the 64 banks) is its physical index mod 16,
-// since rows are multiples of 256 bytes at D >= 128; at D = 64 and 32 a 256-byte line holds
-// 2 and 4 rows.  At D = 256 a row is two bank
+// since rows are multiples of 256 bytes at D >= 128; at D = 64, 32 and 16 a 256-byte line
+// holds 2, 4 and 8 rows.  At D = 256 a row is two bank
 // lines; the XOR values stay below 16, so they keep a chunk's high bit and give the
 // same bank pattern as at D = 128.
 template <int D, int BN>

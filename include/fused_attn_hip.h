@@ -94,8 +94,7 @@ typedef struct fa_fwd_params {
 /* Dense FA2 forward.  Replaces attention_fwd_mma (csrc/bindings.cpp:63-81),
    run_attention_fwd_mma (csrc/flash_attn.h:27), attention_fwd (the SIMT kernel,
    csrc/flash_attn.cu:222-228) and attention_triton (fused_attn/triton_fwd.py:225-265).
-   f16/bf16 with D in {32, 64, 128, 256} run on MFMA; f32 (any D) and f16/bf16 D=16 on the
-   generic fp32-math kernel. */
+   f16/bf16 run on MFMA; f32 on the generic fp32-math kernel.  D in {16, 32, 64, 128, 256}. */
 fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
 
 /* Packed variable-length forward.  Replaces attention_varlen_triton

@@ -38,7 +38,8 @@ def _tensor(shape, dtype, bnhd):
 def test_fuzz_dense(seed):
     rng = random.Random(seed)
     dtype, d = rng.choice([(torch.bfloat16, 64), (torch.bfloat16, 128), (torch.float16, 64), (torch.float16, 128),
-                           (torch.bfloat16, 32), (torch.float16, 256), (torch.float32, 64), (torch.float32, 16)])
+                           (torch.bfloat16, 32), (torch.float16, 256), (torch.float32, 64), (torch.float32, 16),
+                           (torch.bfloat16, 16), (torch.float16, 32)])
     hkv = rng.choice([1, 2, 4])
     hq = hkv * rng.choice([1, 2, 4, 8])
     b = rng.randint(1, 3)

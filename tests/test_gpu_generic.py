@@ -1,5 +1,5 @@
-"""The generic HIP kernel (fp32 at every head dim, and head dim 16 in any dtype) vs the
-fp32 oracle; 16-bit D=32 and D=256 cases in this matrix run on the MFMA kernel.
+"""The generic HIP kernel (fp32 at every head dim) vs the fp32 oracle; the 16-bit cases in this
+matrix (D=16, 32, 256) run on the MFMA kernel.
 
 Mirrors the reference's fused-kernel matrix (tests/test_correctness.py:53-85): fp32 at
 atol = rtol = 1e-4, fp16 / bf16 at the build's bars; plus its fp32 custom-scale and

@@ -28,7 +28,7 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("head_dim", [32, 64, 128, 256])
+@pytest.mark.parametrize("head_dim", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k", SHAPES)
 def test_prefill_matches_oracle(b, h_q, h_kv, n_q, n_k, causal, head_dim, dtype):
@@ -121,7 +121,7 @@ def test_zero_sized_inputs():
 
 
 def test_unsupported_head_dim_raises_loudly():
-    q = randn(1, 2, 16, 48, dtype=torch.bfloat16)  # fp32 and 16-bit D=16 go to the generic kernel
+    q = randn(1, 2, 16, 48, dtype=torch.bfloat16)  # fp32 goes to the generic kernel at D in {16, ..., 256}
     with pytest.raises(RuntimeError, match="unsupported"):
         _hip.fwd(q, q, q)
 
@@ -133,6 +133,7 @@ def test_unsupported_head_dim_raises_loudly():
     dict(b=4, hq=32, hkv=8, n=4096, d=128, layout="bhnd"),
     dict(b=4, hq=16, hkv=16, n=4096, d=64, layout="bhnd"),
     dict(b=4, hq=16, hkv=16, n=4096, d=32, layout="bhnd"),
+    dict(b=4, hq=16, hkv=16, n=4096, d=16, layout="bhnd"),
     dict(b=4, hq=32, hkv=8, n=4096, d=128, layout="bnhd"),
 ])
 def test_benchmark_prefill_workloads(cfg):
@@ -184,25 +185,27 @@ def test_head_dim_256_views_varlen_and_decode_shapes(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_head_dim_32_views_varlen_and_decode_shapes(dtype):
-    """D=32 on the MFMA kernel (128-key tiles of 8 KiB, no V swizzle): the [B,N,H,D] view, a varlen
-    batch with an empty sequence and LSE, and a decode-shaped call (split-K does not take D=32)."""
-    announce(f"d=32 extra shapes {dtype}")
+@pytest.mark.parametrize("d", [16, 32])
+def test_small_head_dims_views_varlen_and_decode_shapes(d, dtype):
+    """D=32 and D=16 on the MFMA kernel (128-key tiles; at D=16 the V tile is padded to 32 columns):
+    the [B,N,H,D] view, a varlen batch with an empty sequence, and a decode-shaped call (split-K
+    does not take these head dims)."""
+    announce(f"d={d} extra shapes {dtype}")
     torch.manual_seed(0)
-    x = randn(2, 300, 3, 4, 32, dtype=dtype)
+    x = randn(2, 300, 3, 4, d, dtype=dtype)
     q, k, v = (x[:, :, i].transpose(1, 2) for i in range(3))
     out = fused_attn.attention(q, k, v, causal=True)
     assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=True)) <= TOL[dtype]
     lens = [37, 0, 300, 1, 129]
-    qv, cu, mx = fused_attn.pack_varlen([randn(n, 8, 32, dtype=dtype) for n in lens])
-    kv, _, _ = fused_attn.pack_varlen([randn(n, 2, 32, dtype=dtype) for n in lens])
-    vv, _, _ = fused_attn.pack_varlen([randn(n, 2, 32, dtype=dtype) for n in lens])
+    qv, cu, mx = fused_attn.pack_varlen([randn(n, 8, d, dtype=dtype) for n in lens])
+    kv, _, _ = fused_attn.pack_varlen([randn(n, 2, d, dtype=dtype) for n in lens])
+    vv, _, _ = fused_attn.pack_varlen([randn(n, 2, d, dtype=dtype) for n in lens])
     out = fused_attn.attention_varlen(qv, kv, vv, cu, cu, mx, mx, causal=True)
     ref = orc.attention_varlen(qv.cpu(), kv.cpu(), vv.cpu(), cu.cpu(), cu.cpu(), causal=True)
     assert max_err(out, ref) <= TOL[dtype]
-    q = randn(2, 8, 1, 32, dtype=dtype)
-    k = randn(2, 2, 3000, 32, dtype=dtype)
-    v = randn(2, 2, 3000, 32, dtype=dtype)
+    q = randn(2, 8, 1, d, dtype=dtype)
+    k = randn(2, 2, 3000, d, dtype=dtype)
+    v = randn(2, 2, 3000, d, dtype=dtype)
     assert ops._hip_kernel_for(q, k) == "fwd"
     assert max_err(fused_attn.attention(q, k, v), orc.attention(q.cpu(), k.cpu(), v.cpu())) <= TOL[dtype]
 
