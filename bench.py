@@ -35,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "cuda-attention-kernels_amd"))
 
 MFMA_BF16_PEAK_TFLOPS = 2516.6
+MFMA_FP32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA peak of MI355X
 HBM_PEAK_GBS = 8000.0
 PREFILL = dict(b=4, hq=32, hkv=8, n=4096, d=128)
 DECODE = dict(b=32, hq=32, hkv=8, nk=32768, d=128)
@@ -119,7 +120,8 @@ def bench_prefill_extras(steps, warmup):
         out = fn()
         assert not torch.isnan(out).any()
         wall, ev = _time_calls(fn, steps, warmup)
-        res[name] = {"workload": workload, "ms": round(wall * 1e3, 4), "TFLOP_s": round(flops / wall / 1e12, 1),
+        res[name] = {"workload": workload, "ms": round(wall * 1e3, 4), "ms_events": round(ev * 1e3, 4),
+                     "TFLOP_s": round(flops / wall / 1e12, 1),
                      "TFLOP_s_events": round(flops / ev / 1e12, 1),
                      "mfma_frac": round(flops / ev / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
 
@@ -142,6 +144,14 @@ def bench_prefill_extras(steps, warmup):
     entry("prefill_d256_gqa", "causal GQA prefill B=2 Hq=16 Hkv=4 N=4096 D=256 bf16",
           lambda: fused_attn.attention(q, k, v, causal=True), attn_flops(2, 16, 4096, 256, True))
     c = PREFILL
+    q = torch.randn(c["b"], c["hq"], c["n"], c["d"], device="cuda", generator=g)
+    k = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g)
+    v = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g)
+    flops = attn_flops(c["b"], c["hq"], c["n"], c["d"], True)
+    entry("prefill_fp32", f"causal GQA prefill B={c['b']} Hq={c['hq']} Hkv={c['hkv']} N={c['n']} D={c['d']} fp32",
+          lambda: fused_attn.attention(q, k, v, causal=True), flops)
+    res["prefill_fp32"]["mfma_fp32_frac"] = round(flops / (res["prefill_fp32"]["ms_events"] * 1e-3) / 1e12
+                                                  / MFMA_FP32_PEAK_TFLOPS, 4)
     q = torch.randn(c["b"], c["n"], c["hq"], c["d"], device="cuda", generator=g).bfloat16().transpose(1, 2)
     k = torch.randn(c["b"], c["n"], c["hkv"], c["d"], device="cuda", generator=g).bfloat16().transpose(1, 2)
     v = torch.randn(c["b"], c["n"], c["hkv"], c["d"], device="cuda", generator=g).bfloat16().transpose(1, 2)

@@ -18,7 +18,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_OUT = os.path.join(HERE, "fused_attn", "libfused_attn_hip.so")
-SOURCES = ["fa_prefill.hip", "fa_splitk.hip", "fa_generic.hip", "fa_quant.hip", "fa_abi.cpp"]
+SOURCES = ["fa_prefill.hip", "fa_prefill_f32.hip", "fa_splitk.hip", "fa_generic.hip", "fa_quant.hip", "fa_abi.cpp"]
 ARCH = os.environ.get("FUSED_ATTN_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -40,7 +40,7 @@ size_t dtype_bytes(int32_t dt) {
 
 // Validation shared by every forward entry point.  `fp8_ok` allows FP8 K/V (split-K);
 // `generic_ok` also allows fp32 and head dims 16 and 32 (prefill and varlen, where the MFMA kernel
-// takes 16-bit D in {16, 32, 64, 128, 256} and the generic kernel takes fp32).
+// takes 16-bit D in {16, 32, 64, 128, 256} and fp32 runs on the fp32 MFMA kernel or the generic one).
 fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok, bool generic_ok) {
   if (p == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params is NULL");
   if (p->batch < 0 || p->heads_q <= 0 || p->heads_kv <= 0 || p->seqlen_q < 0 || p->seqlen_k < 0 ||

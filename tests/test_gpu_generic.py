@@ -1,5 +1,5 @@
-"""The generic HIP kernel (fp32 at every head dim) vs the fp32 oracle; the 16-bit cases in this
-matrix (D=16, 32, 256) run on the MFMA kernel.
+"""The fp32 kernels (the generic kernel at D=16, 32 and 256, the fp32-MFMA kernel at D=64 and 128)
+vs the fp32 oracle; the 16-bit cases in this matrix (D=16, 32, 256) run on the 16-bit MFMA kernel.
 
 Mirrors the reference's fused-kernel matrix (tests/test_correctness.py:53-85): fp32 at
 atol = rtol = 1e-4, fp16 / bf16 at the build's bars; plus its fp32 custom-scale and
@@ -99,14 +99,16 @@ def test_generic_varlen(dtype, d, causal):
     _check(out, ref, dtype)
 
 
+@pytest.mark.parametrize("d", [32, 128])
 @pytest.mark.parametrize("causal", [False, True])
-def test_generic_lse_fp32(causal):
-    announce(f"generic fp32 lse causal={causal}")
+def test_generic_lse_fp32(causal, d):
+    """fp32 LSE on the generic kernel (D=32) and on the fp32-MFMA kernel (D=128)."""
+    announce(f"fp32 lse causal={causal} d={d}")
     torch.manual_seed(0)
-    q = randn(2, 4, 50, 32, dtype=torch.float32)
-    k = randn(2, 2, 40, 32, dtype=torch.float32)
+    q = randn(2, 4, 50, d, dtype=torch.float32)
+    k = randn(2, 2, 40, d, dtype=torch.float32)
     out, lse = _hip.fwd(q, k, k, causal=causal, return_lse=True)
-    s = torch.matmul(q.cpu(), orc.expand_kv(k.cpu(), 2).transpose(-1, -2)) / math.sqrt(32)
+    s = torch.matmul(q.cpu(), orc.expand_kv(k.cpu(), 2).transpose(-1, -2)) / math.sqrt(d)
     if causal:
         s = s.masked_fill(~orc.causal_mask(50, 40), float("-inf"))
     ref = torch.logsumexp(s, dim=-1)
