@@ -68,3 +68,15 @@ def test_fp32_mfma_long_causal():
     out = fused_attn.attention(q, k, v, causal=True)
     ref = orc.attention_chunked(q, k, v, causal=True, heads_per_chunk=1, rows_per_chunk=512)
     torch.testing.assert_close(out, ref, **TOL)
+
+
+def test_reference_cpu_configuration_on_the_gpu():
+    """The reference's CPU-runnable case: dense causal MHA fp32 B=2 Hq=Hkv=4 N=256 D=64, seed 0,
+    scale 1/sqrt(D), [B,H,N,D].  Runs on the fp32-MFMA kernel and matches the oracle at 1e-4."""
+    announce("reference cpu configuration fp32 B=2 H=4 N=256 D=64")
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(2, 4, 256, 64) for _ in range(3))
+    out = fused_attn.attention(q.cuda(), k.cuda(), v.cuda(), causal=True)
+    torch.testing.assert_close(out.cpu(), orc.attention(q, k, v, causal=True), **TOL)
+    torch.testing.assert_close(out.cpu(), torch.from_numpy(orc.attention_f64(q, k, v, causal=True)).float(),
+                               **TOL)
