@@ -600,20 +600,39 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
   // Online merge of partials sg, sg + SPB, ...: (m, l, acc) with acc and l relative to 2^m.
   // An empty partial (m_s = -inf, l_s = 0) gets weight 0; m stays -inf until a partial
   // with keys arrives, and the -inf guards keep 2^(-inf - -inf) out of the sums.
+  // Partials are loaded CH at a time before any is merged, so that CH loads per thread are in
+  // flight at once (the compiler kept a load-then-merge loop at one load in flight; measured:
+  // the D=256 decode merge over 256 partitions went from 13.0 to 8.9 us, the D=128 merges
+  // did not change).  Slots past the last partial take the empty partial (m = -inf, l = 0),
+  // which merges as a no-op.
+  constexpr int CH = 8;
   float m = NEG_INF, l = 0.f;
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-  for (int s = sg; s < S; s += SPB) {
-    const f32x2 st = __builtin_bit_cast(f32x2, ld8(ml + 2 * s));
-    const u32x4 pv = ld16(op + (int64_t)s * D + 8 * dq);
-    const float m_new = fmaxf(m, st[0]);
-    const float m_ref = (m_new == NEG_INF) ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_ref);  // 0 while m = -inf
-    const float w = fast_exp2(st[0] - m_ref) * st[1];
-    l = l * alpha + w;
-    acc0 = acc0 * alpha + w * f32x4{lo_f32<E>(pv[0]), hi_f32<E>(pv[0]), lo_f32<E>(pv[1]), hi_f32<E>(pv[1])};
-    acc1 = acc1 * alpha + w * f32x4{lo_f32<E>(pv[2]), hi_f32<E>(pv[2]), lo_f32<E>(pv[3]), hi_f32<E>(pv[3])};
-    m = m_new;
+  for (int s0 = sg; s0 < S; s0 += CH * SPB) {
+    f32x2 st[CH];
+    u32x4 pv[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int s = s0 + u * SPB;
+      if (s < S) {
+        st[u] = __builtin_bit_cast(f32x2, ld8(ml + 2 * s));
+        pv[u] = ld16(op + (int64_t)s * D + 8 * dq);
+      } else {
+        st[u] = f32x2{NEG_INF, 0.f};
+        pv[u] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const float m_new = fmaxf(m, st[u][0]);
+      const float m_ref = (m_new == NEG_INF) ? 0.f : m_new;
+      const float alpha = fast_exp2(m - m_ref);  // 0 while m = -inf
+      const float w = fast_exp2(st[u][0] - m_ref) * st[u][1];
+      l = l * alpha + w;
+      acc0 = acc0 * alpha + w * f32x4{lo_f32<E>(pv[u][0]), hi_f32<E>(pv[u][0]), lo_f32<E>(pv[u][1]), hi_f32<E>(pv[u][1])};
+      acc1 = acc1 * alpha + w * f32x4{lo_f32<E>(pv[u][2]), hi_f32<E>(pv[u][2]), lo_f32<E>(pv[u][3]), hi_f32<E>(pv[u][3])};
+      m = m_new;
+    }
   }
   part[sg][dq][0] = acc0;
   part[sg][dq][1] = acc1;
