@@ -1,4 +1,4 @@
-// fp32 FlashAttention-2 prefill on the fp32 matrix cores of MI355X (gfx950), D in {64, 128}.
+// fp32 FlashAttention-2 prefill on the fp32 matrix cores of MI355X (gfx950), D in {32, 64, 128}.
 //
 // Serves fp32 Q/K/V: the role of the reference's SIMT kernel attn_fwd_kernel
 // (csrc/flash_attn.cu:54-187) and of its Triton kernel's fp32 inputs
@@ -18,11 +18,13 @@
 //  - O^T += V^T P^T over 16 steps of k = 2.  Step r uses, in lane (j, g), the key
 //    8(r/4) + 4g + r%4: the one whose probability the lane holds in register r, so P never
 //    moves between lanes.  A = V^T, where row i of d block b is d = DB*i + b (DB = D/32
-//    blocks), so one 16-byte (D=128) or 8-byte (D=64) LDS read of a V row feeds the step's
-//    DB MFMAs.
-//  - K tiles keep 16-byte chunk c of row n at c ^ (n % 16): the 16 rows of one read pass hit
-//    16 different bank groups.  A pass over V reads 256 contiguous bytes of one row, so V
-//    needs no swizzle.
+//    blocks), so one 16-byte (D=128), 8-byte (D=64) or 4-byte (D=32) LDS read of a V row
+//    feeds the step's DB MFMAs.
+//  - K tiles keep 16-byte chunk c of row n at c ^ swz(n), swz(n) = n % 16 (D >= 64) or
+//    (n / 2) % 8 (D = 32, whose 128-byte rows put two rows on one bank line): the 16 rows of
+//    one read pass hit 16 different bank groups.  A pass over V reads whole rows, so V needs
+//    no swizzle (at D=32 the two row halves of a wave share banks: a 2-way conflict on
+//    4-byte reads, small beside the 64-cycle MFMAs they feed).
 #include <float.h>
 
 #include <type_traits>
@@ -47,7 +49,7 @@ attn_fwd_f32_kernel(const TileArgs a) {
   constexpr int QPW = TILE * 4 / 1024 / NW;   // 1-KiB DMA blocks per wave per tile
   constexpr int DB = D / 32;                  // 32-row d blocks of O^T
   constexpr int HS = D / 2;                   // k = 2 steps of S^T
-  static_assert(D == 64 || D == 128, "head dim");
+  static_assert(D == 32 || D == 64 || D == 128, "head dim");
   static_assert(TILE * 4 % (1024 * NW) == 0, "direct loads must split evenly over the waves");
   constexpr float NEG_INF = -__builtin_inff();
 
@@ -120,6 +122,8 @@ attn_fwd_f32_kernel(const TileArgs a) {
     }
   }
 
+  auto swz = [](int n) __attribute__((always_inline)) { return D >= 64 ? n % 16 : (n >> 1) & 7; };
+
   // ---- K/V tiles: global -> LDS (loads past the tile's last valid key return zeros) -----
   const uint8_t* kbase = (const uint8_t*)a.k + ((int64_t)b * a.skb + (int64_t)kvh * a.skh + ktok0 * a.skn) * 4;
   const uint8_t* vbase = (const uint8_t*)a.v + ((int64_t)b * a.svb + (int64_t)kvh * a.svh + ktok0 * a.svn) * 4;
@@ -137,7 +141,7 @@ attn_fwd_f32_kernel(const TileArgs a) {
       const int blk = wave * QPW + i;
       const int byte = blk * 1024 + lane * 16;
       const int r = byte / (D * 4), p = (byte % (D * 4)) / 16;
-      lds_dma16<false>(rk, (uint8_t*)kd + blk * 1024, r * (int)krow_bytes + ((p ^ (r % 16)) * 16));
+      lds_dma16<false>(rk, (uint8_t*)kd + blk * 1024, r * (int)krow_bytes + ((p ^ swz(r)) * 16));
       lds_dma16<false>(rv, (uint8_t*)vd + blk * 1024, r * (int)vrow_bytes + p * 16);
     }
   };
@@ -153,7 +157,7 @@ attn_fwd_f32_kernel(const TileArgs a) {
     f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
     for (int s4 = 0; s4 < HS / 4; ++s4) {
-      const int chunk = (g * (HS / 4) + s4) ^ (j % 16);
+      const int chunk = (g * (HS / 4) + s4) ^ swz(j);
       const f32x4 kv = __builtin_bit_cast(f32x4, ld16(Ks + j * D + chunk * 4));
       s0 = mfma_f32(kv[0], qreg[4 * s4 + 0], s0);
       s1 = mfma_f32(kv[1], qreg[4 * s4 + 1], s1);
@@ -197,10 +201,12 @@ attn_fwd_f32_kernel(const TileArgs a) {
         const f32x4 w = __builtin_bit_cast(f32x4, ld16(vp));
 #pragma unroll
         for (int d = 0; d < 4; ++d) oacc[d] = mfma_f32(w[d], p[r], oacc[d]);
-      } else {
+      } else if constexpr (DB == 2) {
         const f32x2 w = __builtin_bit_cast(f32x2, ld8(vp));
 #pragma unroll
         for (int d = 0; d < 2; ++d) oacc[d] = mfma_f32(w[d], p[r], oacc[d]);
+      } else {
+        oacc[0] = mfma_f32(*vp, p[r], oacc[0]);
       }
     }
   };
@@ -234,10 +240,14 @@ attn_fwd_f32_kernel(const TileArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int i = 8 * (r >> 2) + 4 * g + (r & 3);  // O^T row of register r: d = DB*i + block
+    if constexpr (DB == 1) {
+      op[i] = oacc[0][r] * inv;
+    } else {
 #pragma unroll
-    for (int d = 0; d < DB; d += 2) {
-      st8(op + DB * i + d, u32x2{__builtin_bit_cast(uint32_t, oacc[d][r] * inv),
-                                 __builtin_bit_cast(uint32_t, oacc[d + 1][r] * inv)});
+      for (int d = 0; d < DB; d += 2) {
+        st8(op + DB * i + d, u32x2{__builtin_bit_cast(uint32_t, oacc[d][r] * inv),
+                                   __builtin_bit_cast(uint32_t, oacc[d + 1][r] * inv)});
+      }
     }
   }
   if (a.lse != nullptr && g == 0) {
@@ -278,7 +288,9 @@ fa_status run_fwd_f32(const fa_fwd_params& p, bool varlen, hipStream_t stream, c
     return FA_ERR_UNSUPPORTED;
   }
   a.total = (int32_t)total;
-  const hipError_t e = p.head_dim == 128 ? launch_f32<128>(a, stream) : launch_f32<64>(a, stream);
+  const hipError_t e = p.head_dim == 128 ? launch_f32<128>(a, stream)
+                       : p.head_dim == 64 ? launch_f32<64>(a, stream)
+                                          : launch_f32<32>(a, stream);
   return hip_status(e, err);
 }
 
