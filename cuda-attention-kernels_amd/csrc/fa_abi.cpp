@@ -88,10 +88,12 @@ fa_status validate(const fa_fwd_params* p, bool varlen, bool fp8_ok, bool generi
     return fail(FA_ERR_INVALID_ARGUMENT, "k/v strides must be multiples of 16 bytes");
   if ((!varlen && (p->o_stride_b % ovec)) || p->o_stride_h % ovec || p->o_stride_n % ovec)
     return fail(FA_ERR_INVALID_ARGUMENT, "o strides must be multiples of 8 bytes");
-  // K/V tiles are addressed with 32-bit byte offsets of up to 64 rows from the tile start
+  // K/V tiles are addressed with signed 32-bit byte offsets of up to 128 rows (the prefill
+  // kernel's tiles at D <= 64) from the tile start: 127 rows of a stride below 16 MiB stay
+  // below 2^31
   const int64_t kvb = (int64_t)dtype_bytes(p->kv_dtype);
-  if (p->k_stride_n < 0 || p->v_stride_n < 0 || p->k_stride_n * kvb >= (1 << 25) || p->v_stride_n * kvb >= (1 << 25))
-    return fail(FA_ERR_UNSUPPORTED, "k/v token stride must be below 32 MiB");
+  if (p->k_stride_n < 0 || p->v_stride_n < 0 || p->k_stride_n * kvb >= (1 << 24) || p->v_stride_n * kvb >= (1 << 24))
+    return fail(FA_ERR_UNSUPPORTED, "k/v token stride must be below 16 MiB");
   return FA_OK;
 }
 

@@ -51,7 +51,8 @@ typedef enum fa_status {
  * varlen, LSE and FP8 fields the Triton paths carried as kernel arguments.
  *
  * Dense layout:  q [B, Hq, Nq, D], k/v [B, Hkv, Nk, D], o like q, any strides
- *                with unit stride along D (strides are in elements).
+ *                with unit stride along D (strides are in elements); k/v token
+ *                strides below 16 MiB.
  * Varlen layout: q [total_q, Hq, D], k/v [total_k, Hkv, D]; `batch` is the
  *                number of sequences, cu_seqlens_q/k are device int32 arrays
  *                of batch+1 prefix offsets starting at 0, the *_stride_b

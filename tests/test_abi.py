@@ -89,6 +89,8 @@ def _params(**over):
     (dict(dtype=9), _hip.FA_ERR_INVALID_ARGUMENT, "unknown dtype"),
     (dict(scale=float("nan")), _hip.FA_ERR_INVALID_ARGUMENT, "NaN"),
     (dict(k_stride_n=1 << 24), _hip.FA_ERR_UNSUPPORTED, "token stride"),
+    # 128-key tiles: 127 rows of a 16 MiB stride would overflow a signed 32-bit byte offset
+    (dict(v_stride_n=1 << 23), _hip.FA_ERR_UNSUPPORTED, "token stride"),
 ])
 def test_fwd_validation(lib, over, code, msg):
     p = _params(**over)
