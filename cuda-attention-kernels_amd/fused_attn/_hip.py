@@ -226,6 +226,9 @@ def _check(status: int, what: str) -> None:
 # ----------------------------------------------------------------------------------------------
 
 
+TOKEN_STRIDE_LIMIT_BYTES = 1 << 24  # the C ABI's bound on K/V token strides
+
+
 def _aligned_view(t: torch.Tensor, vec_elems: int, base_align: int) -> torch.Tensor:
     """``t`` itself when its D stride is 1 and its pointer/other strides allow the kernels'
     vector accesses, else a contiguous copy (the kernels never see an unaligned view)."""
@@ -235,6 +238,12 @@ def _aligned_view(t: torch.Tensor, vec_elems: int, base_align: int) -> torch.Ten
             if t.size(i) > 1 and t.stride(i) % vec_elems != 0:
                 ok = False
                 break
+    # The kernels address up to 128 K/V rows from a tile start with 32-bit byte offsets, and the
+    # C ABI rejects token strides of 16 MiB or more: such a view is copied too.  The token dim is
+    # 2 of [B, H, N, D] and 0 of a packed [T, H, D].
+    tok = 2 if t.dim() == 4 else 0
+    if ok and t.dim() >= 3 and t.size(tok) > 1 and t.stride(tok) * t.element_size() >= TOKEN_STRIDE_LIMIT_BYTES:
+        ok = False
     # clone, not contiguous(): an already-contiguous view at an unaligned offset must be copied too
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 

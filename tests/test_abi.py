@@ -341,3 +341,16 @@ def test_paged_split_spanning_too_many_pages_is_rejected(lib):
 def test_paged_empty_requests_succeed_without_launch(lib):
     assert _paged_call(lib, p=_params(batch=0, seqlen_q=1, seqlen_k=200)) == _hip.FA_OK
     assert _paged_call(lib, p=_params(seqlen_q=0, seqlen_k=200)) == _hip.FA_OK
+
+
+def test_views_with_token_strides_past_the_abi_bound_are_copied():
+    """The C ABI rejects K/V token strides of 16 MiB or more; the Python layer hands such views to
+    the kernels as contiguous copies instead, so callers never see that bound."""
+    base = torch.zeros(2 * (1 << 23), dtype=torch.bfloat16)  # 32 MiB
+    at_bound = base.as_strided((1, 1, 2, 64), (0, 0, 1 << 23, 1))  # [B, H, N, D], 16 MiB token stride
+    below = base.as_strided((1, 1, 2, 64), (0, 0, (1 << 23) - 8, 1))
+    packed = base.as_strided((2, 1, 64), (1 << 23, 0, 1))  # [T, H, D]
+    for view in (at_bound, packed):
+        out = _hip._aligned_view(view, 8, 16)
+        assert out.data_ptr() != view.data_ptr() and out.is_contiguous() and torch.equal(out, view)
+    assert _hip._aligned_view(below, 8, 16) is below
