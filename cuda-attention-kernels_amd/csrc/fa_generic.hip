@@ -1,6 +1,6 @@
 // Generic FlashAttention-2 forward for the shapes the MFMA kernels do not take:
-// fp32 Q/K/V (computed in fp32 throughout) at head dims 16 and 256 (32, 64 and 128 run on the
-// fp32 MFMA kernel).  The kernel also accepts every head dim and 16-bit storage.  This is the role of the reference's SIMT kernel
+// fp32 Q/K/V (computed in fp32 throughout) at head dim 16 (32 to 256 run on the fp32 MFMA
+// kernel).  The kernel also accepts every head dim and 16-bit storage.  This is the role of the reference's SIMT kernel
 // attn_fwd_kernel (csrc/flash_attn.cu:54-187) and of its Triton kernel's other head
 // dims (fused_attn/triton_fwd.py:210-222): same semantics as the MFMA prefill kernel
 // (bottom-right causal mask, GQA, varlen, natural-log LSE, zero rows without keys).

@@ -75,9 +75,9 @@ inline fa_status hip_status(hipError_t e, const char** err) {
 
 // Launchers.  They assume fa_abi.cpp has validated `p`.
 fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
-// fp32 at head dims 16 and 256 (fa_generic.hip); run_fwd forwards those here.
+// fp32 at head dim 16 (fa_generic.hip); run_fwd forwards it here.
 fa_status run_fwd_generic(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
-// fp32 at head dims 32, 64 and 128 on the fp32 MFMA (fa_prefill_f32.hip); run_fwd forwards those here.
+// fp32 at head dims 32 to 256 on the fp32 MFMA (fa_prefill_f32.hip); run_fwd forwards those here.
 fa_status run_fwd_f32(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
 fa_status run_quantize_fp8(const fa_quant_params& p, hipStream_t stream, const char** err);
 // kv: paged K/V (nullptr for a dense cache)

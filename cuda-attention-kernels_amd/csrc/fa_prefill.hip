@@ -472,7 +472,7 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
   const bool mfma = (p.dtype == FA_DTYPE_BF16 || p.dtype == FA_DTYPE_F16) &&
                     (p.head_dim == 16 || p.head_dim == 32 || p.head_dim == 64 || p.head_dim == 128 ||
                      p.head_dim == 256);
-  if (p.dtype == FA_DTYPE_F32 && (p.head_dim == 32 || p.head_dim == 64 || p.head_dim == 128))
+  if (p.dtype == FA_DTYPE_F32 && p.head_dim >= 32)
     return run_fwd_f32(p, varlen, stream, err);
   if (!mfma) return run_fwd_generic(p, varlen, stream, err);
   TileArgs a = common_args(p);

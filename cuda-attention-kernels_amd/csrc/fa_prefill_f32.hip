@@ -1,4 +1,4 @@
-// fp32 FlashAttention-2 prefill on the fp32 matrix cores of MI355X (gfx950), D in {32, 64, 128}.
+// fp32 FlashAttention-2 prefill on the fp32 matrix cores of MI355X (gfx950), D in {32, 64, 128, 256}.
 //
 // Serves fp32 Q/K/V: the role of the reference's SIMT kernel attn_fwd_kernel
 // (csrc/flash_attn.cu:54-187) and of its Triton kernel's fp32 inputs
@@ -18,8 +18,9 @@
 //  - O^T += V^T P^T over 16 steps of k = 2.  Step r uses, in lane (j, g), the key
 //    8(r/4) + 4g + r%4: the one whose probability the lane holds in register r, so P never
 //    moves between lanes.  A = V^T, where row i of d block b is d = DB*i + b (DB = D/32
-//    blocks), so one 16-byte (D=128), 8-byte (D=64) or 4-byte (D=32) LDS read of a V row
-//    feeds the step's DB MFMAs.
+//    blocks), so one LDS read of a V row (32 bytes at D=256 down to 4 at D=32) feeds the
+//    step's DB MFMAs.  At D=256 the fp32 accumulators and half a Q row take 256 registers, so
+//    that variant runs one wave per SIMD.
 //  - K tiles keep 16-byte chunk c of row n at c ^ swz(n), swz(n) = n % 16 (D >= 64) or
 //    (n / 2) % 8 (D = 32, whose 128-byte rows put two rows on one bank line): the 16 rows of
 //    one read pass hit 16 different bank groups.  A pass over V reads whole rows, so V needs
@@ -41,7 +42,7 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
 }
 
 template <int D>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 attn_fwd_f32_kernel(const TileArgs a) {
   constexpr int NW = 4;
   constexpr int BN = 32;                      // keys per tile: one 32-key MFMA block
@@ -49,7 +50,7 @@ attn_fwd_f32_kernel(const TileArgs a) {
   constexpr int QPW = TILE * 4 / 1024 / NW;   // 1-KiB DMA blocks per wave per tile
   constexpr int DB = D / 32;                  // 32-row d blocks of O^T
   constexpr int HS = D / 2;                   // k = 2 steps of S^T
-  static_assert(D == 32 || D == 64 || D == 128, "head dim");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dim");
   static_assert(TILE * 4 % (1024 * NW) == 0, "direct loads must split evenly over the waves");
   constexpr float NEG_INF = -__builtin_inff();
 
@@ -197,7 +198,14 @@ attn_fwd_f32_kernel(const TileArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float* vp = Vs + (8 * (r >> 2) + 4 * g + (r & 3)) * D + DB * j;
-      if constexpr (DB == 4) {
+      if constexpr (DB == 8) {
+        const f32x4 w0 = __builtin_bit_cast(f32x4, ld16(vp)), w1 = __builtin_bit_cast(f32x4, ld16(vp + 4));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          oacc[d] = mfma_f32(w0[d], p[r], oacc[d]);
+          oacc[d + 4] = mfma_f32(w1[d], p[r], oacc[d + 4]);
+        }
+      } else if constexpr (DB == 4) {
         const f32x4 w = __builtin_bit_cast(f32x4, ld16(vp));
 #pragma unroll
         for (int d = 0; d < 4; ++d) oacc[d] = mfma_f32(w[d], p[r], oacc[d]);
@@ -288,7 +296,8 @@ fa_status run_fwd_f32(const fa_fwd_params& p, bool varlen, hipStream_t stream, c
     return FA_ERR_UNSUPPORTED;
   }
   a.total = (int32_t)total;
-  const hipError_t e = p.head_dim == 128 ? launch_f32<128>(a, stream)
+  const hipError_t e = p.head_dim == 256 ? launch_f32<256>(a, stream)
+                       : p.head_dim == 128 ? launch_f32<128>(a, stream)
                        : p.head_dim == 64 ? launch_f32<64>(a, stream)
                                           : launch_f32<32>(a, stream);
   return hip_status(e, err);

@@ -95,8 +95,8 @@ typedef struct fa_fwd_params {
 /* Dense FA2 forward.  Replaces attention_fwd_mma (csrc/bindings.cpp:63-81),
    run_attention_fwd_mma (csrc/flash_attn.h:27), attention_fwd (the SIMT kernel,
    csrc/flash_attn.cu:222-228) and attention_triton (fused_attn/triton_fwd.py:225-265).
-   f16/bf16 run on the 16-bit MFMA kernel; f32 on the fp32 MFMA at D in {32, 64, 128} and on
-   the generic fp32-math kernel at D in {16, 256}.  D in {16, 32, 64, 128, 256}. */
+   f16/bf16 run on the 16-bit MFMA kernel; f32 on the fp32 MFMA at D in {32, 64, 128, 256} and
+   on the generic fp32-math kernel at D = 16.  D in {16, 32, 64, 128, 256}. */
 fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
 
 /* Packed variable-length forward.  Replaces attention_varlen_triton

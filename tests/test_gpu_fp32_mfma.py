@@ -1,4 +1,4 @@
-"""The fp32-MFMA prefill kernel (fp32 Q/K/V, D = 32, 64 and 128) vs the fp32 oracle at the reference's
+"""The fp32-MFMA prefill kernel (fp32 Q/K/V, D = 32, 64, 128 and 256) vs the fp32 oracle at the reference's
 fp32 bar, atol = rtol = 1e-4 (tests/test_correctness.py:53-85): several key tiles, ragged tails,
 GQA/MQA, bottom-right causal alignment with rows that see no key, [B,N,H,D] views, negative scale,
 packed sequences with empty ones, and a long causal sequence."""
@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 TOL = dict(atol=1e-4, rtol=1e-4)
 
 
-@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k", [
     (1, 4, 4, 129, 129),   # one 128-query block plus one row, 5 key tiles
@@ -33,7 +33,7 @@ def test_fp32_mfma_matches_oracle(b, h_q, h_kv, n_q, n_k, causal, d):
     torch.testing.assert_close(out.cpu(), orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal), **TOL)
 
 
-@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 def test_fp32_mfma_views_and_scales(d):
     announce(f"fp32 mfma [B,N,H,D] view and scales d={d}")
     torch.manual_seed(1)
@@ -45,7 +45,7 @@ def test_fp32_mfma_views_and_scales(d):
                                    **TOL)
 
 
-@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 def test_fp32_mfma_varlen(d, causal):
     announce(f"fp32 mfma varlen d={d} causal={causal}")

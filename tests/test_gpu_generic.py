@@ -1,4 +1,4 @@
-"""The fp32 kernels (the generic kernel at D=16 and 256, the fp32-MFMA kernel at D=32, 64 and 128)
+"""The fp32 kernels (the generic kernel at D=16, the fp32-MFMA kernel at D=32, 64, 128 and 256)
 vs the fp32 oracle; the 16-bit cases in this matrix (D=16, 32, 256) run on the 16-bit MFMA kernel.
 
 Mirrors the reference's fused-kernel matrix (tests/test_correctness.py:53-85): fp32 at
