@@ -33,6 +33,7 @@
 
 #include "fa_device.hpp"
 #include "fa_internal.hpp"
+#include "fa_prefill_common.hpp"
 #include "fa_tile.hpp"
 
 namespace fa {
@@ -71,50 +72,10 @@ attn_fwd_kernel(const TileArgs a) {
   __shared__ __align__(16) uint16_t v_buf0[VTILE];
   __shared__ __align__(16) uint16_t v_buf1[VTILE];
 
-  // ---- work item: (batch, q-head, 128-query block) -----------------------------------
-  // Scheduling units: the q-heads of as many kv-heads as keep about kL2UnitBytes of
-  // K/V (one XCD's L2 is 4 MB).  Units follow each other in logical order, and
-  // xcd_remap hands each XCD a contiguous range of logical indices, so an XCD works
-  // through one or two units at a time and re-reads K/V from its L2.  Inside a unit
-  // the query blocks go by rank, heaviest causal blocks first, all heads of the unit
-  // at each rank, which keeps the XCD's CUs evenly loaded to the end.
-  //
-  // Varlen batches are the exception: their sequences differ in length, and ranges of
-  // whole sequences per XCD load the XCDs unevenly (measured: a 16-sequence batch ran at
-  // 0.18 of peak).  There the order is rank-major per XCD: the dispatcher deals workgroups
-  // to the XCDs round-robin (blockIdx % 8), XCD x takes the (sequence, kv-head) groups
-  // g = x (mod 8) and walks them rank by rank, heaviest causal ranks first, with the q-heads
-  // of one kv-head side by side, so they run together and read its K/V through one L2
-  // (measured: +8-10% over rank-major across all XCDs, which fetched each K/V tile into up
-  // to four L2s).  The host pads the grid to a multiple of 8 groups; padding exits here.
-  constexpr int64_t kL2UnitBytes = int64_t{4} << 20;
-  constexpr int kXcds = 8;
-  int mrev, item;
-  if (a.varlen) {
-    const int xcd = (int)blockIdx.x % kXcds, local = (int)blockIdx.x / kXcds;
-    const int per_rank = a.total / (a.n_rowblk * kXcds);  // this XCD's (group, q-head) items per rank
-    mrev = local / per_rank;
-    const int j = local % per_rank;
-    const int kvg = (j / a.group) * kXcds + xcd;
-    if (kvg >= a.kv_groups) return;  // grid padding (uniform over the workgroup)
-    item = kvg * a.group + j % a.group;
-  } else {
-    const int nbh = a.total / a.n_rowblk;  // (batch, q-head) pairs
-    const int logical = xcd_remap((int)blockIdx.x, a.total);
-    const int64_t kv_head_bytes = (int64_t)max(a.nk, 1) * D * 2 * 2;
-    const int unit_heads = max(1, (int)(kL2UnitBytes / kv_head_bytes)) * a.group;
-    const int unit = logical / (unit_heads * a.n_rowblk);
-    const int within = logical % (unit_heads * a.n_rowblk);
-    const int unit_size = min(unit_heads, nbh - unit * unit_heads);
-    mrev = within / unit_size;
-    item = unit * unit_heads + within % unit_size;
-  }
-  const int gi = item % a.group;
-  item /= a.group;
-  const int kvh = item % a.hkv;
-  const int b = item / a.hkv;
-  const int hq = kvh * a.group + gi;
-  const int rb = a.causal ? (a.n_rowblk - 1 - mrev) : mrev;  // heaviest causal blocks first
+  // ---- work item: (batch, q-head, NW*32-query block) ----------------------------------
+  PrefillItem it;
+  if (!prefill_item<D>(a, it)) return;  // grid padding (uniform over the workgroup)
+  const int b = it.b, hq = it.hq, kvh = it.kvh, rb = it.rb;
 
   int seq_q = a.nq, seq_k = a.nk;
   int64_t qtok0 = 0, ktok0 = 0;
