@@ -1,6 +1,7 @@
-// Generic FlashAttention-2 forward for the shapes the MFMA kernels do not take:
-// fp32 Q/K/V (computed in fp32 throughout) at head dim 16 (32 to 256 run on the fp32 MFMA
-// kernel).  The kernel also accepts every head dim and 16-bit storage.  This is the role of the reference's SIMT kernel
+// Generic FlashAttention-2 forward for the one shape the MFMA kernels do not take: fp32
+// Q/K/V (computed in fp32 throughout) at head dim 16 (fp32 at 32 to 256 runs on the fp32 MFMA
+// kernel, 16-bit storage on the 16-bit MFMA kernel).  The template is written for any storage
+// type and head dim, but only <float, 16> is instantiated.  This is the role of the reference's SIMT kernel
 // attn_fwd_kernel (csrc/flash_attn.cu:54-187) and of its Triton kernel's other head
 // dims (fused_attn/triton_fwd.py:210-222): same semantics as the MFMA prefill kernel
 // (bottom-right causal mask, GQA, varlen, natural-log LSE, zero rows without keys).
@@ -173,24 +174,6 @@ static hipError_t launch_generic(const TileArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <class T>
-static hipError_t launch_generic_d(const TileArgs& a, int d, hipStream_t stream) {
-  switch (d) {
-    case 16:
-      return launch_generic<T, 16>(a, stream);
-    case 32:
-      return launch_generic<T, 32>(a, stream);
-    case 64:
-      return launch_generic<T, 64>(a, stream);
-    case 128:
-      return launch_generic<T, 128>(a, stream);
-    case 256:
-      return launch_generic<T, 256>(a, stream);
-    default:
-      return hipErrorInvalidValue;
-  }
-}
-
 fa_status run_fwd_generic(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err) {
   TileArgs a = common_args(p);
   a.o = p.o;
@@ -216,21 +199,12 @@ fa_status run_fwd_generic(const fa_fwd_params& p, bool varlen, hipStream_t strea
     return FA_ERR_UNSUPPORTED;
   }
   a.total = (int32_t)total;
-  hipError_t e = hipErrorInvalidValue;
-  switch (p.dtype) {
-    case FA_DTYPE_F32:
-      e = launch_generic_d<float>(a, p.head_dim, stream);
-      break;
-    case FA_DTYPE_BF16:
-      e = launch_generic_d<__bf16>(a, p.head_dim, stream);
-      break;
-    case FA_DTYPE_F16:
-      e = launch_generic_d<_Float16>(a, p.head_dim, stream);
-      break;
-    default:
-      break;
+  // run_fwd sends only fp32 at head dim 16 here
+  if (p.dtype != FA_DTYPE_F32 || p.head_dim != 16) {
+    *err = "the generic kernel serves fp32 at head_dim 16 only";
+    return FA_ERR_UNSUPPORTED;
   }
-  return hip_status(e, err);
+  return hip_status(launch_generic<float, 16>(a, stream), err);
 }
 
 }  // namespace fa

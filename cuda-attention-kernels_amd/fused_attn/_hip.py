@@ -248,6 +248,36 @@ def _aligned_view(t: torch.Tensor, vec_elems: int, base_align: int) -> torch.Ten
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: str, kv_fp8: bool = False) -> None:
+    """Reject q/k/v that do not describe one attention problem before anything is launched
+    (the reference's check_inputs, csrc/bindings.cpp:35-44, and _check, triton_fwd.py:217-222):
+    the kernels take head_dim and the batch from q and the K/V dtype, lengths and heads from k,
+    so a V of another shape or dtype, or a K of another head_dim, would be read out of bounds.
+
+    layout: "dense" q [B,Hq,Nq,D], k/v [B or 1,Hkv,Nk,D]; "varlen" q [Tq,Hq,D], k/v [Tk,Hkv,D];
+    "paged" q [B,Hq,Nq,D], k/v pools [P,Hkv,page,D]."""
+    nd = 3 if layout == "varlen" else 4
+    if q.dim() != nd or k.dim() != nd or v.dim() != nd:
+        raise RuntimeError(f"expected {nd}-D q, k and v for the {layout} layout, got "
+                           f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if k.shape != v.shape:
+        raise RuntimeError(f"k and v must have the same shape, got {tuple(k.shape)} and {tuple(v.shape)}")
+    if k.dtype != v.dtype:
+        raise RuntimeError(f"k and v must have the same dtype, got {k.dtype} and {v.dtype}")
+    if kv_fp8:
+        if k.dtype != _FP8:
+            raise RuntimeError(f"FP8 K/V must be float8_e4m3fn, got {k.dtype}")
+    elif q.dtype != k.dtype:
+        raise RuntimeError(f"q/k/v dtypes must match, got {q.dtype} and {k.dtype}")
+    if q.shape[-1] != k.shape[-1]:
+        raise RuntimeError(f"q and k must have the same head_dim, got {q.shape[-1]} and {k.shape[-1]}")
+    hq, hkv = q.shape[-2 if layout == "varlen" else 1], k.shape[-2 if layout == "varlen" else 1]
+    if hkv == 0 or hq % hkv != 0:
+        raise RuntimeError(f"H_q ({hq}) must be a multiple of H_kv ({hkv})")
+    if layout == "dense" and k.shape[0] not in (q.shape[0], 1):
+        raise RuntimeError(f"k/v batch ({k.shape[0]}) must equal q's ({q.shape[0]}) or be 1")
+
+
 def _prep_qkv(q, k, v, kv_fp8: bool = False):
     q = _aligned_view(q, 8, 16)
     kv_vec = 16 if kv_fp8 else 8
@@ -333,6 +363,7 @@ def _require_gpu(*ts: torch.Tensor) -> None:
 def fwd(q, k, v, causal: bool = False, scale: Optional[float] = None, return_lse: bool = False,
         out: Optional[torch.Tensor] = None):
     """Dense FA2 forward.  q [B,Hq,Nq,D]; k, v [B,Hkv,Nk,D]; returns o (and natural-log LSE [B,Hq,Nq])."""
+    _check_qkv(q, k, v, "dense")
     _require_gpu(q, k, v)
     lib = load_library()
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
@@ -351,6 +382,7 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqle
 
     With ``return_lse`` also returns the natural-log LSE as fp32 [Hq, Tq]; rows of tokens outside every
     sequence are left unwritten (like the output rows)."""
+    _check_qkv(q, k, v, "varlen")
     _require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k)
     if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
         raise RuntimeError("cu_seqlens must be int32")
@@ -372,6 +404,34 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqle
     return (o, lse) if return_lse else o
 
 
+def _check_fp8_scales(k: torch.Tensor, k_scale, v_scale) -> None:
+    """FP8 block scales must be [B_k, Hkv, ceil(Nk / 64)] floats on k's device
+    (fused_attn/fp8.py:31-45): the kernel indexes them by (batch, kv-head, 64-key block)."""
+    if k_scale is None or v_scale is None:
+        raise RuntimeError("FP8 K/V needs k_scale and v_scale")
+    want = (k.shape[0], k.shape[1], -(-k.shape[2] // FP8_QBLOCK))
+    for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if tuple(t.shape) != want:
+            raise RuntimeError(f"{name} must have shape {want} (per 64-key block of k), got {tuple(t.shape)}")
+        if not t.is_floating_point() or t.dtype == _FP8:
+            raise RuntimeError(f"{name} must be a float tensor, got {t.dtype}")
+        if t.device != k.device:
+            raise RuntimeError(f"{name} must be on {k.device}, got {t.device}")
+
+
+def _prep_fp8_scales(k: torch.Tensor, k_scale, v_scale):
+    """FP8 block scales as the kernel reads them: fp32 with unit stride along the blocks and the
+    same strides for both.  Scales of another float dtype are converted: the kernel reads raw
+    fp32 words."""
+    if k_scale.dtype != torch.float32 or k_scale.stride(-1) != 1:
+        k_scale = k_scale.to(torch.float32).contiguous()
+    if v_scale.dtype != torch.float32 or v_scale.stride(-1) != 1:
+        v_scale = v_scale.to(torch.float32).contiguous()
+    if k_scale.stride() != v_scale.stride():
+        k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()
+    return k_scale, v_scale
+
+
 def split_len_for(seqlen_k: int, num_splits: int, block: int = FP8_QBLOCK) -> int:
     """Split length rounded up to whole ``block``-key tiles (triton_splitk.py:153-154)."""
     num_splits = max(1, int(num_splits))
@@ -383,16 +443,16 @@ def splitk(q, k, v, causal: bool = False, scale: Optional[float] = None, split_l
            k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None,
            workspace: Optional[torch.Tensor] = None):
     """Split-K flash-decoding + LSE combine.  k/v may be float8_e4m3fn with per-64-key fp32 scales."""
+    fp8 = _FP8 is not None and k.dtype == _FP8
+    _check_qkv(q, k, v, "dense", kv_fp8=fp8)
+    if fp8:
+        _check_fp8_scales(k, k_scale, v_scale)
     _require_gpu(q, k, v)
     lib = load_library()
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
-    fp8 = _FP8 is not None and k.dtype == _FP8
     q, k, v = _prep_qkv(q, k, v, kv_fp8=fp8)
     if fp8:
-        k_scale = k_scale.float().contiguous() if k_scale.stride(-1) != 1 else k_scale
-        v_scale = v_scale.float().contiguous() if v_scale.stride(-1) != 1 else v_scale
-        if k_scale.stride() != v_scale.stride():
-            k_scale, v_scale = k_scale.contiguous(), v_scale.contiguous()
+        k_scale, v_scale = _prep_fp8_scales(k, k_scale, v_scale)
     o = _new_output(q)
     b, hq, nq, d = q.shape
     nk = k.shape[2]
@@ -412,14 +472,15 @@ def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int,
                  scale: Optional[float] = None, split_len: int = 128, workspace: Optional[torch.Tensor] = None):
     """Split-K decode over a paged cache.  q [B,Hq,Nq,D]; k_cache/v_cache [num_pages, Hkv, page_size, D]
     (any strides with unit D stride); block_table int32 [B, cols]; seqlens_k int32 [B], both on the GPU."""
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4:
+        raise RuntimeError("k_cache and v_cache must both be [num_pages, Hkv, page_size, D]")
+    _check_qkv(q, k_cache, v_cache, "paged")
     _require_gpu(q, k_cache, v_cache, block_table, seqlens_k)
     if block_table.dtype != torch.int32 or seqlens_k.dtype != torch.int32:
         raise RuntimeError("block_table and seqlens_k must be int32")
     if block_table.dim() != 2 or seqlens_k.dim() != 1 or block_table.shape[0] != q.shape[0] \
             or seqlens_k.shape[0] != q.shape[0]:
         raise RuntimeError("block_table must be [B, pages] and seqlens_k [B] for q's batch B")
-    if k_cache.shape != v_cache.shape or k_cache.dim() != 4:
-        raise RuntimeError("k_cache and v_cache must both be [num_pages, Hkv, page_size, D]")
     lib = load_library()
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
     q, k_cache, v_cache = _prep_qkv(q, k_cache, v_cache)
