@@ -128,8 +128,8 @@ size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_
                                  int32_t num_splits) {
   if (batch <= 0 || heads_q <= 0 || seqlen_q <= 0 || head_dim <= 0 || num_splits <= 0) return 0;
   const size_t rows = (size_t)batch * (size_t)heads_q * (size_t)seqlen_q * (size_t)num_splits;
-  // 16-bit normalised partial outputs, then fp32 (max, sum) pairs
-  return rows * ((size_t)head_dim * 2 + 2 * sizeof(float));
+  // fp32 normalised partial outputs, then fp32 (max, sum) pairs
+  return rows * ((size_t)head_dim * sizeof(float) + 2 * sizeof(float));
 }
 
 fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace, size_t workspace_bytes,
@@ -137,7 +137,8 @@ fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* w
   g_last_error.clear();
   fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/true, /*generic_ok=*/false);
   if (st != FA_OK) return st;
-  if (p->lse != nullptr) return fail(FA_ERR_UNSUPPORTED, "LSE output is not available on the split-K path");
+  if (p->lse != nullptr && (p->lse_stride_b < 0 || p->lse_stride_h < 0))
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
   if (split_len <= 0 || split_len % 64 != 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "split_len must be a positive multiple of 64");
   if (p->batch == 0 || p->seqlen_q == 0) return FA_OK;
@@ -166,7 +167,8 @@ fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* k
   q.k_stride_b = q.v_stride_b = 0;  // keys are found through the block table
   fa_status st = validate(&q, /*varlen=*/false, /*fp8_ok=*/false, /*generic_ok=*/false);
   if (st != FA_OK) return st;
-  if (q.lse != nullptr) return fail(FA_ERR_UNSUPPORTED, "LSE output is not available on the split-K path");
+  if (q.lse != nullptr && (q.lse_stride_b < 0 || q.lse_stride_h < 0))
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
   if (split_len <= 0 || split_len % 64 != 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "split_len must be a positive multiple of 64");
   if (kv->page_size <= 0 || kv->page_size % 32 != 0)

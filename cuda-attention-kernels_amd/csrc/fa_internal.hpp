@@ -16,7 +16,7 @@ struct TileArgs {
   const void* q;
   const void* k;
   const void* v;
-  void* o;     // prefill: output in the q dtype; split-K: 16-bit partials [rows, S, D]
+  void* o;     // prefill: output in the q dtype; split-K: fp32 partials [rows, S, D]
   float* ml;   // split-K: (max, sum) pairs [rows, S, 2]
   float* lse;  // prefill: optional natural-log LSE
   const float* k_scale;
@@ -53,10 +53,12 @@ struct QuantArgs {
 };
 
 struct CombineArgs {
-  const uint16_t* opart;  // normalised partials in the output's 16-bit type
+  const float* opart;  // normalised fp32 partials
   const float* ml;
   void* o;
   int64_t sob, soh, son;
+  float* lse;  // optional natural-log LSE [B, Hq, Nq]
+  int64_t slb, slh;
   int32_t hq, nq, n_split;
 };
 

@@ -3,11 +3,10 @@
 //   * attn_splitk_kernel: the reference's _attn_splitk_kernel
 //     (fused_attn/triton_splitk.py:29-96), including the FP8 K/V variant of
 //     _attn_fp8_kernel (fused_attn/fp8.py:59-122): one partial output per key
-//     partition plus its (max, sum) statistics in the log2 domain.  The reference
-//     keeps un-normalised fp32 partials; here a partial is normalised by its own sum
-//     (a convex combination of V rows) and stored in Q's 16-bit type, which halves
-//     the partial traffic (a 128-key partition writes and re-reads D * 2 bytes per
-//     row instead of D * 4) at the cost of one 16-bit rounding;
+//     partition plus its (max, sum) statistics in the log2 domain.  Partials are fp32,
+//     as the reference keeps them (triton_splitk.py:90-96,156-158), so the combine adds
+//     no rounding beyond fp32; each is stored normalised by its own sum (a convex
+//     combination of V rows, O_s / l_s), which the combine weighs by l_s;
 //   * splitk_combine_kernel: the log-sum-exp merge of the partitions
 //     (_splitk_combine_kernel, fused_attn/triton_splitk.py:99-127).
 //
@@ -173,9 +172,23 @@ attn_splitk_kernel(const TileArgs a) {
   const int64_t krow_bytes = a.skn * KV::bytes, vrow_bytes = a.svn * KV::bytes;
   const float* ksc = nullptr;
   const float* vsc = nullptr;
+  // FP8: P is multiplied by v_scale / v_ref before its 16-bit rounding, with v_ref the largest
+  // V block scale of this workgroup's keys, and v_ref goes back in, in fp32, when a partial is
+  // emitted.  The reference applies v_scale after the product, in fp32 (fp8.py:104,116);
+  // folding v_scale itself into P would push P * v_scale (v_scale = amax / 448) below fp16's
+  // normal range for V of small magnitude.  The ratio is at most 1, and only blocks whose
+  // weight is negligible beside the largest lose bits.
+  float v_ref = 1.f;
   if (KV::bytes == 1) {
     ksc = a.k_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
     vsc = a.v_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
+    const int blo = klo / 64, bhi = khi > klo ? (khi + 63) / 64 : blo;
+    float vm = 0.f;
+    for (int bk = blo + (int)(threadIdx.x & 63); bk < bhi; bk += 64) vm = fmaxf(vm, vsc[bk]);
+    vm = max_xor32(vm);
+#pragma unroll
+    for (int sh = 16; sh >= 1; sh >>= 1) vm = fmaxf(vm, __shfl_xor(vm, sh, 64));
+    v_ref = fmaxf(vm, FLT_MIN);
   }
 
   // A negative softmax scale is applied by negating Q (exact for 16-bit floats),
@@ -338,22 +351,22 @@ attn_splitk_kernel(const TileArgs a) {
   }
   const int qlim = qi + offset;  // last key this lane's row may see (causal)
 
-  // Partial of partition `part`, normalised by its row sum and rounded to E, plus its
-  // log2-domain statistics (triton_splitk.py:90-96); then the state restarts for the
-  // next partition.  A partition with no visible key (l = 0) stores zeros.
+  // Partial of partition `part` in fp32, normalised by its row sum, plus its log2-domain
+  // statistics (triton_splitk.py:90-96); then the state restarts for the next partition.
+  // A partition with no visible key (l = 0) stores zeros.
   auto emit_partial = [&](int part) __attribute__((always_inline)) {
     const float l_tot = sum_xor32(l_run);  // each lane summed its 16 of the row's keys per tile
     if (wave_active && row_ok) {
       const int64_t prow = ((int64_t)(b * a.hq + hq) * seq_q + qi) * a.n_split + part;
-      uint16_t* op = (uint16_t*)a.o + prow * D;
-      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      float* op = (float*)a.o + prow * D;
+      const float inv = l_tot > 0.f ? v_ref / l_tot : 0.f;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
-          const int d0 = d * 32 + 8 * rq + 4 * g;
-          st8(op + d0, u32x2{pack2<E>(oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv),
-                             pack2<E>(oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv)});
+          const int d0 = d * 32 + 8 * rq + 4 * g;  // this lane's 4 consecutive elements
+          st16(op + d0, __builtin_bit_cast(u32x4, f32x4{oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv,
+                                                         oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv}));
         }
       }
       if (g == 0) st8(a.ml + prow * 2, __builtin_bit_cast(u32x2, f32x2{m_run, l_tot}));
@@ -413,7 +426,7 @@ attn_splitk_kernel(const TileArgs a) {
       if constexpr (KV::bytes == 1) {
         const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
         sc[kb] = fmaxf(c_abs * ksc[blk], kMinScale);
-        vs[kb] = vsc[blk];
+        vs[kb] = vsc[blk] / v_ref;
       } else {
         sc[kb] = c_abs;
         vs[kb] = 1.f;
@@ -471,7 +484,7 @@ attn_splitk_kernel(const TileArgs a) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         if constexpr (KV::bytes == 1) {
-          // v_scale folded into P (the reference scales P.V by v_scale, fp8.py:116)
+          // v_scale / v_ref folded into P (v_ref is restored when the partial is emitted)
           const float v = vs[kb];
 #pragma unroll
           for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
@@ -575,11 +588,11 @@ attn_splitk_kernel(const TileArgs a) {
   for (int part = part0 + (n_tiles + tiles_per_part - 1) / tiles_per_part; part < part_end; ++part) emit_partial(part);
 }
 
-// Log-sum-exp merge of split-K partials (triton_splitk.py:99-127), with each partial
+// Log-sum-exp merge of split-K partials (triton_splitk.py:99-127), with each fp32 partial
 // O_s stored normalised (O_s = un-normalised partial / l_s):
 //   m = max_s m_s;  w_s = 2^(m_s - m) l_s;  O = sum_s w_s O_s / sum_s w_s   (0 when the sum is 0)
-// One 256-thread workgroup per output row; D/8 threads cover a partial row with 16-byte
-// loads (8 elements), so 256/(D/8) partials are read concurrently.  Each thread merges
+// One 256-thread workgroup per output row; D/8 threads cover a partial row with two 16-byte
+// loads each (8 elements), so 256/(D/8) partials are read concurrently.  Each thread merges
 // its partials online (running max, rescaled sums), and the threads' (m, l, acc) triples
 // are merged through LDS at the end: one pass over the partials, no separate max pass.
 template <int D, class E>
@@ -593,7 +606,7 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
   const int64_t row = blockIdx.x;  // (b, hq, qi) flattened
   const int S = c.n_split;
   const float* ml = c.ml + row * S * 2;
-  const uint16_t* op = c.opart + row * (int64_t)S * D;
+  const float* op = c.opart + row * (int64_t)S * D;
   const int tid = (int)threadIdx.x;
   const int sg = tid / TPS, dq = tid % TPS;
 
@@ -610,16 +623,17 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = sg; s0 < S; s0 += CH * SPB) {
     f32x2 st[CH];
-    u32x4 pv[CH];
+    f32x4 pv0[CH], pv1[CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int s = s0 + u * SPB;
       if (s < S) {
         st[u] = __builtin_bit_cast(f32x2, ld8(ml + 2 * s));
-        pv[u] = ld16(op + (int64_t)s * D + 8 * dq);
+        pv0[u] = __builtin_bit_cast(f32x4, ld16(op + (int64_t)s * D + 8 * dq));
+        pv1[u] = __builtin_bit_cast(f32x4, ld16(op + (int64_t)s * D + 8 * dq + 4));
       } else {
         st[u] = f32x2{NEG_INF, 0.f};
-        pv[u] = u32x4{0u, 0u, 0u, 0u};
+        pv0[u] = pv1[u] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
 #pragma unroll
@@ -629,8 +643,8 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
       const float alpha = fast_exp2(m - m_ref);  // 0 while m = -inf
       const float w = fast_exp2(st[u][0] - m_ref) * st[u][1];
       l = l * alpha + w;
-      acc0 = acc0 * alpha + w * f32x4{lo_f32<E>(pv[u][0]), hi_f32<E>(pv[u][0]), lo_f32<E>(pv[u][1]), hi_f32<E>(pv[u][1])};
-      acc1 = acc1 * alpha + w * f32x4{lo_f32<E>(pv[u][2]), hi_f32<E>(pv[u][2]), lo_f32<E>(pv[u][3]), hi_f32<E>(pv[u][3])};
+      acc0 = acc0 * alpha + w * pv0[u];
+      acc1 = acc1 * alpha + w * pv1[u];
       m = m_new;
     }
   }
@@ -652,11 +666,14 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
       t0 += a * part[k][tid][0];
       t1 += a * part[k][tid][1];
     }
-    const float inv = 1.f / ((lt == 0.f) ? 1.f : lt);
+    const float l_safe = (lt == 0.f) ? 1.f : lt;
+    const float inv = 1.f / l_safe;
     const int qi = (int)(row % c.nq);
     const int64_t bh = row / c.nq;
     const int hq = (int)(bh % c.hq);
     const int64_t b = bh / c.hq;
+    // natural-log LSE of the row (triton_fwd.py:169-172): m and the weights are relative to 2^m_ref
+    if (c.lse != nullptr && tid == 0) c.lse[b * c.slb + (int64_t)hq * c.slh + qi] = (mx + __log2f(l_safe)) * kLn2;  // -inf for a row without keys, as the prefill kernel
     uint16_t* o = (uint16_t*)c.o + b * c.sob + (int64_t)hq * c.soh + (int64_t)qi * c.son + 8 * tid;
     st8(o, u32x2{pack2<E>(t0[0] * inv, t0[1] * inv), pack2<E>(t0[2] * inv, t0[3] * inv)});
     st8(o + 4, u32x2{pack2<E>(t1[0] * inv, t1[1] * inv), pack2<E>(t1[2] * inv, t1[3] * inv)});
@@ -790,8 +807,8 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
     return FA_ERR_UNSUPPORTED;
   }
   a.total = (int32_t)total;
-  a.o = workspace;  // 16-bit partials [rows, S, D], then (m, l) pairs [rows, S, 2]
-  a.ml = (float*)((uint8_t*)workspace + out_rows * S * p.head_dim * 2);
+  a.o = workspace;  // fp32 partials [rows, S, D], then (m, l) pairs [rows, S, 2]
+  a.ml = (float*)((uint8_t*)workspace + out_rows * S * p.head_dim * 4);
   const bool fp8 = p.kv_dtype == FA_DTYPE_FP8_E4M3;
   const bool bf = p.dtype == FA_DTYPE_BF16;
   hipError_t e = hipErrorInvalidValue;
@@ -806,7 +823,7 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
   if (e != hipSuccess) return hip_status(e, err);
 
   CombineArgs c{};
-  c.opart = (const uint16_t*)a.o;
+  c.opart = (const float*)a.o;
   c.ml = a.ml;
   c.o = p.o;
   c.sob = p.o_stride_b;
@@ -815,6 +832,9 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
   c.hq = p.heads_q;
   c.nq = p.seqlen_q;
   c.n_split = S;
+  c.lse = p.lse;
+  c.slb = p.lse_stride_b;
+  c.slh = p.lse_stride_h;
   if (p.head_dim == 128) {
     e = bf ? launch_combine<128, BF16>(c, out_rows, stream) : launch_combine<128, F16>(c, out_rows, stream);
   } else if (p.head_dim == 256) {

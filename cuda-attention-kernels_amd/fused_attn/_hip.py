@@ -22,7 +22,7 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libfused_attn_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # fa_dtype codes
 F16, BF16, F32, FP8_E4M3 = 0, 1, 2, 3
@@ -441,8 +441,9 @@ def split_len_for(seqlen_k: int, num_splits: int, block: int = FP8_QBLOCK) -> in
 
 def splitk(q, k, v, causal: bool = False, scale: Optional[float] = None, split_len: int = 128,
            k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None,
-           workspace: Optional[torch.Tensor] = None):
-    """Split-K flash-decoding + LSE combine.  k/v may be float8_e4m3fn with per-64-key fp32 scales."""
+           workspace: Optional[torch.Tensor] = None, return_lse: bool = False):
+    """Split-K flash-decoding + LSE combine.  k/v may be float8_e4m3fn with per-64-key fp32 scales.
+    With ``return_lse`` also returns the natural-log LSE, fp32 [B, Hq, Nq] (-inf for rows without keys)."""
     fp8 = _FP8 is not None and k.dtype == _FP8
     _check_qkv(q, k, v, "dense", kv_fp8=fp8)
     if fp8:
@@ -460,18 +461,22 @@ def splitk(q, k, v, causal: bool = False, scale: Optional[float] = None, split_l
     need = lib.fa_splitk_workspace_bytes(b, hq, nq, d, splits)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=q.device)
-    p = make_params(q, k, v, o, causal, scale, k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None)
+    lse = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if return_lse else None
+    p = make_params(q, k, v, o, causal, scale, k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None,
+                    lse=lse)
     with torch.cuda.device(q.device):
         _check(lib.fa_attention_splitk(ctypes.byref(p), int(split_len), ctypes.c_void_p(workspace.data_ptr()),
                                        workspace.numel() * workspace.element_size(),
                                        ctypes.c_void_p(_stream(q))), "attention_splitk")
-    return o
+    return (o, lse) if return_lse else o
 
 
 def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int, causal: bool = False,
-                 scale: Optional[float] = None, split_len: int = 128, workspace: Optional[torch.Tensor] = None):
+                 scale: Optional[float] = None, split_len: int = 128, workspace: Optional[torch.Tensor] = None,
+                 return_lse: bool = False):
     """Split-K decode over a paged cache.  q [B,Hq,Nq,D]; k_cache/v_cache [num_pages, Hkv, page_size, D]
-    (any strides with unit D stride); block_table int32 [B, cols]; seqlens_k int32 [B], both on the GPU."""
+    (any strides with unit D stride); block_table int32 [B, cols]; seqlens_k int32 [B], both on the GPU.
+    With ``return_lse`` also returns the natural-log LSE, fp32 [B, Hq, Nq]."""
     if k_cache.shape != v_cache.shape or k_cache.dim() != 4:
         raise RuntimeError("k_cache and v_cache must both be [num_pages, Hkv, page_size, D]")
     _check_qkv(q, k_cache, v_cache, "paged")
@@ -493,7 +498,8 @@ def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int,
     need = lib.fa_splitk_workspace_bytes(b, hq, nq, d, splits)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=q.device)
-    p = make_params(q, k_cache, v_cache, o, causal, scale)
+    lse = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if return_lse else None
+    p = make_params(q, k_cache, v_cache, o, causal, scale, lse=lse)
     p.seqlen_k = max_k
     p.k_stride_b = p.v_stride_b = 0
     kv = PagedKV()
@@ -506,7 +512,7 @@ def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int,
                                              ctypes.c_void_p(workspace.data_ptr()),
                                              workspace.numel() * workspace.element_size(),
                                              ctypes.c_void_p(_stream(q))), "attention_paged_decode")
-    return o
+    return (o, lse) if return_lse else o
 
 
 def choose_num_splits(batch: int, heads: int, seqlen_k: int, seqlen_q: int, num_cus: int) -> int:

@@ -26,7 +26,7 @@ import torch
 
 from . import _hip
 from .ops import _pick_backend
-from .reference import attention_reference
+from .reference import attention_reference, lse_reference
 
 QBLOCK = 64  # keys per scale
 E4M3_MAX = 448.0
@@ -82,15 +82,18 @@ def attention_fp8(
     causal: bool = False,
     scale: Optional[float] = None,
     split_len: Optional[int] = None,
-) -> torch.Tensor:
-    """Attention over an FP8 K/V cache (reference signature: fused_attn/fp8.py:125-128, plus ``split_len``)."""
+    return_lse: bool = False,
+):
+    """Attention over an FP8 K/V cache (reference signature: fused_attn/fp8.py:125-128, plus ``split_len``
+    and ``return_lse``: the natural-log LSE fp32 [B, H_q, N_q] of the scores on the dequantised keys)."""
     assert q.dtype in (torch.float16, torch.bfloat16), \
         "Q must be fp16/bf16 (FP8 is converted to Q's dtype for the MFMA)"
     assert k8.dtype == FP8_DTYPE and v8.dtype == FP8_DTYPE
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
     if not q.is_cuda:
-        return attention_reference(q, dequantize_kv_fp8(k8, k_scale), dequantize_kv_fp8(v8, v_scale),
-                                   causal=causal, scale=scale)
+        kd = dequantize_kv_fp8(k8, k_scale)
+        o = attention_reference(q, kd, dequantize_kv_fp8(v8, v_scale), causal=causal, scale=scale)
+        return (o, lse_reference(q, kd, causal=causal, scale=scale)) if return_lse else o
     if split_len is None:
         if q.shape[-2] <= 16:  # decode-shaped: partitions sized for the grid (ops.default_split_len)
             from .ops import default_split_len
@@ -99,7 +102,7 @@ def attention_fp8(
         else:  # prefill-shaped: one partition, as the reference's single-pass kernel (fp8.py:136-145)
             split_len = max(QBLOCK, -(-k8.shape[-2] // QBLOCK) * QBLOCK)
     return _hip.splitk(q, k8, v8, causal=causal, scale=scale, split_len=int(split_len), k_scale=k_scale,
-                       v_scale=v_scale)
+                       v_scale=v_scale, return_lse=return_lse)
 
 
 # The reference exported the Triton entry under this name (fused_attn/__init__.py:5-9).

@@ -27,7 +27,7 @@ import torch
 
 from . import _hip
 from .ops import _pick_backend, default_split_len
-from .reference import attention_reference
+from .reference import attention_reference, lse_reference
 
 
 def gather_paged(cache: torch.Tensor, block_table: torch.Tensor, seqlen: int, b: int) -> torch.Tensor:
@@ -39,25 +39,30 @@ def gather_paged(cache: torch.Tensor, block_table: torch.Tensor, seqlen: int, b:
 
 
 def attention_paged_reference(q, k_cache, v_cache, block_table, seqlens_k, causal: bool = False,
-                              scale: Optional[float] = None) -> torch.Tensor:
+                              scale: Optional[float] = None, return_lse: bool = False):
     """Unfused path: gather each sequence's pages, then ``attention_reference`` on it."""
     out = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if return_lse else None
     lens = seqlens_k.tolist()
     for b, n in enumerate(lens):
         k = gather_paged(k_cache, block_table, n, b)[None]
         v = gather_paged(v_cache, block_table, n, b)[None]
         out[b:b + 1] = attention_reference(q[b:b + 1], k, v, causal=causal, scale=scale)
-    return out
+        if return_lse:
+            lse[b:b + 1] = lse_reference(q[b:b + 1], k, causal=causal, scale=scale)
+    return (out, lse) if return_lse else out
 
 
 def attention_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
                     seqlens_k: torch.Tensor, causal: bool = False, scale: Optional[float] = None,
-                    max_seqlen_k: Optional[int] = None, split_len: Optional[int] = None) -> torch.Tensor:
+                    max_seqlen_k: Optional[int] = None, split_len: Optional[int] = None, return_lse: bool = False):
     """Decode attention over a paged K/V cache.  ``max_seqlen_k`` (the largest entry of
-    ``seqlens_k``) sizes the grid; when omitted it is read from ``seqlens_k`` (a device sync)."""
+    ``seqlens_k``) sizes the grid; when omitted it is read from ``seqlens_k`` (a device sync).
+    With ``return_lse`` also returns the natural-log LSE, fp32 [B, H_q, N_q]."""
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
     if not q.is_cuda or _pick_backend(q) != "hip":
-        return attention_paged_reference(q, k_cache, v_cache, block_table, seqlens_k, causal=causal, scale=scale)
+        return attention_paged_reference(q, k_cache, v_cache, block_table, seqlens_k, causal=causal, scale=scale,
+                                         return_lse=return_lse)
     if max_seqlen_k is None:
         max_seqlen_k = int(seqlens_k.max().item()) if seqlens_k.numel() else 0
     if split_len is None:
@@ -68,7 +73,7 @@ def attention_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         page_size = k_cache.shape[2]
         split_len = min(split_len, max(64, (254 * page_size) // 64 * 64))
     return _hip.paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k, causal=causal, scale=scale,
-                             split_len=split_len)
+                             split_len=split_len, return_lse=return_lse)
 
 
 def paged_from_dense(k: torch.Tensor, v: torch.Tensor, page_size: int, seqlens: Optional[list] = None,

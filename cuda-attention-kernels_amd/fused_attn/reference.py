@@ -93,3 +93,19 @@ def attention_varlen_reference(
         )
         out[q0:q1] = o[0].transpose(0, 1)
     return out
+
+
+def lse_reference(q: torch.Tensor, k: torch.Tensor, causal: bool = False, scale: Optional[float] = None) -> torch.Tensor:
+    """Natural-log LSE of the unfused scores [B, H_q, N_q] (the softmax denominator of
+    ``attention_reference``, in log form, as the Triton kernel's WRITE_LSE output,
+    fused_attn/triton_fwd.py:169-172); rows without a visible key are -inf."""
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    g = q.shape[1] // k.shape[1]
+    kk = k.float().repeat_interleave(g, dim=1)
+    s = torch.matmul(q.float(), kk.transpose(-1, -2)) * scale
+    if causal:
+        n_q, n_k = q.shape[-2], k.shape[-2]
+        i = torch.arange(n_q, device=q.device)[:, None]
+        j = torch.arange(n_k, device=q.device)[None, :]
+        s = s.masked_fill(j > i + (n_k - n_q), float("-inf"))
+    return torch.logsumexp(s, dim=-1)

@@ -20,7 +20,7 @@ from typing import Optional
 import torch
 
 from . import _hip
-from .reference import attention_reference
+from .reference import attention_reference, lse_reference
 
 
 def choose_num_splits(batch: int, heads: int, seqlen_k: int, seqlen_q: int, num_sms: int = 108) -> int:
@@ -41,8 +41,11 @@ def attention_splitk(
     scale: Optional[float] = None,
     num_splits: Optional[int] = None,
     split_len: Optional[int] = None,
-) -> torch.Tensor:
-    """Split-K attention (reference signature: triton_splitk.py:140-143, plus ``split_len``).
+    return_lse: bool = False,
+):
+    """Split-K attention (reference signature: triton_splitk.py:140-143, plus ``split_len`` and
+    ``return_lse``, which also returns the natural-log LSE fp32 [B, H_q, N_q] from the combine:
+    the quantity chunked or cascaded decode merges further).
 
     ``num_splits`` is honoured as in the reference: each partition gets
     ``ceil(ceil(n_k / num_splits) / 64) * 64`` keys.  ``split_len`` (a multiple
@@ -54,7 +57,8 @@ def attention_splitk(
     n_k = k.shape[-2]
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     if not q.is_cuda:
-        return attention_reference(q, k, v, causal=causal, scale=scale)
+        o = attention_reference(q, k, v, causal=causal, scale=scale)
+        return (o, lse_reference(q, k, causal=causal, scale=scale)) if return_lse else o
     if split_len is None:
         if num_splits is not None:
             split_len = _hip.split_len_for(n_k, num_splits)
@@ -62,7 +66,7 @@ def attention_splitk(
             from .ops import default_split_len
 
             split_len = default_split_len(q.shape[-2], n_k, q.shape[0], k.shape[1], q.shape[1] // k.shape[1])
-    return _hip.splitk(q, k, v, causal=causal, scale=scale, split_len=int(split_len))
+    return _hip.splitk(q, k, v, causal=causal, scale=scale, split_len=int(split_len), return_lse=return_lse)
 
 
 # The reference exported the Triton entry under this name (fused_attn/__init__.py:5-9).

@@ -9,13 +9,12 @@ LSE as fp32 [H_q, total_q]), which the reference's varlen path did not offer.
 """
 from __future__ import annotations
 
-import math
 from typing import Optional
 
 import torch
 
 from . import _hip
-from .reference import attention_reference, attention_varlen_reference
+from .reference import attention_reference, attention_varlen_reference, lse_reference
 
 
 def attention_triton(
@@ -33,7 +32,7 @@ def attention_triton(
         o = attention_reference(q, k, v, causal=causal, scale=scale)
         if not return_lse:
             return o
-        return o, _lse_reference(q, k, causal, scale)
+        return o, lse_reference(q, k, causal=causal, scale=scale)
     return _hip.fwd(q, k, v, causal=causal, scale=scale, return_lse=return_lse)
 
 
@@ -58,17 +57,3 @@ def attention_varlen_triton(
         return attention_varlen_reference(q, k, v, cu_seqlens_q, cu_seqlens_k, causal=causal, scale=scale)
     return _hip.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, causal=causal,
                            scale=scale, return_lse=return_lse)
-
-
-def _lse_reference(q, k, causal, scale):
-    """Natural-log LSE of the unfused scores (reference.py:36-62 before the softmax); -inf rows stay -inf."""
-    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
-    g = q.shape[1] // k.shape[1]
-    kk = k.float().repeat_interleave(g, dim=1)
-    s = torch.matmul(q.float(), kk.transpose(-1, -2)) * scale
-    if causal:
-        n_q, n_k = q.shape[-2], k.shape[-2]
-        i = torch.arange(n_q, device=q.device)[:, None]
-        j = torch.arange(n_k, device=q.device)[None, :]
-        s = s.masked_fill(j > i + (n_k - n_q), float("-inf"))
-    return torch.logsumexp(s, dim=-1)

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 3
+#define FA_ABI_VERSION 4
 
 /* Element types (reference: DType, csrc/flash_attn.h:7). */
 typedef enum fa_dtype {
@@ -82,7 +82,8 @@ typedef struct fa_fwd_params {
   int32_t max_seqlen_q, max_seqlen_k;
   /* optional natural-log LSE output, fp32 (NULL = not written); reference: WRITE_LSE in
      fused_attn/triton_fwd.py:169-172.  Dense: [B, Hq, Nq] at b*lse_stride_b + h*lse_stride_h + n.
-     Varlen: [Hq, total_q] at h*lse_stride_h + token (lse_stride_b unused); not on split-K. */
+     Varlen: [Hq, total_q] at h*lse_stride_h + token (lse_stride_b unused).  Split-K and paged
+     decode write it from the combine, dense layout.  A row without keys gets -inf. */
   float* lse;
   int64_t lse_stride_b, lse_stride_h;
   /* FP8 K/V block scales, fp32 [B, Hkv, ceil(Nk/64)] (fused_attn/fp8.py:31-45);
@@ -104,19 +105,18 @@ fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
 fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream);
 
 /* Bytes of workspace fa_attention_splitk needs for `num_splits` key partitions:
-   partial outputs [B, Hq, Nq, S, D] in q's 16-bit type, each normalised by its own
-   row sum, plus fp32 (max, sum) pairs [B, Hq, Nq, S, 2] (the reference keeps fp32
-   un-normalised partials: fused_attn/triton_splitk.py:156-158). */
+   fp32 partial outputs [B, Hq, Nq, S, D], each normalised by its own row sum, plus fp32
+   (max, sum) pairs [B, Hq, Nq, S, 2] in the log2 domain (the reference keeps fp32
+   partials too: fused_attn/triton_splitk.py:90-96,156-158). */
 size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q, int32_t head_dim,
                                  int32_t num_splits);
 
-/* Split-K flash-decoding: one pass per `split_len`-key partition writing
-   normalised 16-bit partials and fp32 log2-domain statistics, then a
-   log-sum-exp combine kernel.  f16/bf16 q, D in {64, 128, 256}.  Replaces attention_splitk_triton
-   (fused_attn/triton_splitk.py:140-181) and, with kv_dtype ==
-   FA_DTYPE_FP8_E4M3 and k_scale/v_scale set, attention_fp8_triton
-   (fused_attn/fp8.py:125-147).  split_len must be a positive multiple of 64;
-   num_splits = ceil(seqlen_k / split_len). */
+/* Split-K flash-decoding: one pass per `split_len`-key partition writing normalised fp32
+   partials and fp32 log2-domain statistics, then a log-sum-exp combine kernel (which also
+   writes the optional LSE).  f16/bf16 q, D in {64, 128, 256}.  Replaces attention_splitk_triton
+   (fused_attn/triton_splitk.py:140-181) and, with kv_dtype == FA_DTYPE_FP8_E4M3 and
+   k_scale/v_scale set, attention_fp8_triton (fused_attn/fp8.py:125-147).  split_len must be a
+   positive multiple of 64; num_splits = ceil(seqlen_k / split_len). */
 fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace,
                               size_t workspace_bytes, void* stream);
 

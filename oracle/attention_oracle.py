@@ -22,6 +22,8 @@ How each function is pinned (checked in tests/test_oracle.py):
                        visible key -> zeros; equal scores -> mean of V).
   expand_kv / GQA      vs repeat_interleave + SDPA (tests/test_correctness.py:42-50
                        in the reference).
+  lse                  vs the float64 brute force lse_f64 (-inf rows included), and closed
+                       forms: one visible key -> its scaled score; n equal scores -> s + ln n.
   attention_varlen     vs per-sequence dense attention and the brute force,
                        including zero-length sequences.
   e4m3fn_encode        vs torch's float8_e4m3fn cast on every code, every
@@ -92,6 +94,20 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = 
     p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
     o = torch.matmul(p, vf)
     return o if out_dtype is None else o.to(out_dtype)
+
+
+def lse(q: torch.Tensor, k: torch.Tensor, causal: bool = False, scale: Optional[float] = None) -> torch.Tensor:
+    """Natural-log sum of exp of the scaled scores, fp32 [B, Hq, Nq]: the log of the softmax
+    denominator of ``attention`` (the quantity the reference's Triton kernel writes with
+    WRITE_LSE, fused_attn/triton_fwd.py:169-172).  Rows with no visible key give -inf."""
+    h_q, n_q, d = q.shape[1], q.shape[2], q.shape[3]
+    h_kv, n_k = k.shape[1], k.shape[2]
+    kf = expand_kv(k.float(), h_q // h_kv)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    s = torch.matmul(q.float(), kf.transpose(-1, -2)) * scale
+    if causal:
+        s = s.masked_fill(~causal_mask(n_q, n_k, device=s.device), float("-inf"))
+    return torch.logsumexp(s, dim=-1)
 
 
 def attention_chunked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
@@ -177,6 +193,26 @@ def attention_f64(q, k, v, causal: bool = False, scale: Optional[float] = None) 
                 s = np.array([float(np.dot(q[bi, h, i], kk[j])) * scale for j in range(last)])
                 w = np.exp(s - s.max())
                 out[bi, h, i] = (w[:, None] * vv[:last]).sum(0) / w.sum()
+    return out
+
+
+def lse_f64(q, k, causal: bool = False, scale: Optional[float] = None) -> np.ndarray:
+    """Per-row float64 loops: max + log(sum exp(s - max)) over the visible keys, -inf without any."""
+    q, k = (np.asarray(t.float().cpu() if isinstance(t, torch.Tensor) else t, dtype=np.float64) for t in (q, k))
+    b, h_q, n_q, d = q.shape
+    h_kv, n_k = k.shape[1], k.shape[2]
+    g = h_q // h_kv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    out = np.full((b, h_q, n_q), -np.inf)
+    for bi in range(b):
+        for h in range(h_q):
+            kk = k[bi, h // g]
+            for i in range(n_q):
+                last = n_k if not causal else min(n_k, i + (n_k - n_q) + 1)
+                if last <= 0:
+                    continue
+                s = np.array([float(np.dot(q[bi, h, i], kk[j])) * scale for j in range(last)])
+                out[bi, h, i] = s.max() + math.log(float(np.exp(s - s.max()).sum()))
     return out
 
 

@@ -42,7 +42,7 @@ def test_struct_layout_matches_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _hip.ABI_VERSION == 3
+    assert lib.fa_abi_version() == _hip.ABI_VERSION == 4
 
 
 def test_choose_num_splits_known_answers(lib):
@@ -53,8 +53,8 @@ def test_choose_num_splits_known_answers(lib):
 
 
 def test_workspace_bytes(lib):
-    # 16-bit partials plus fp32 (max, sum) pairs per (row, partition)
-    assert lib.fa_splitk_workspace_bytes(32, 32, 1, 128, 256) == 32 * 32 * 256 * (128 * 2 + 8)
+    # fp32 partials plus fp32 (max, sum) pairs per (row, partition)
+    assert lib.fa_splitk_workspace_bytes(32, 32, 1, 128, 256) == 32 * 32 * 256 * (128 * 4 + 8)
     assert lib.fa_splitk_workspace_bytes(0, 32, 1, 128, 256) == 0
 
 
@@ -168,8 +168,11 @@ def test_splitk_validation(lib):
     fp8 = _params(kv_dtype=_hip.FP8_E4M3, k_stride_n=72, k_scale=0x50000, v_scale=0x50000)
     assert lib.fa_attention_splitk(ctypes.byref(fp8), 64, ctypes.c_void_p(0x40000), need,
                                    None) == _hip.FA_ERR_INVALID_ARGUMENT  # fp8 rows need 16-byte strides
-    p = _params(lse=0x30000)
-    assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need, None) == _hip.FA_ERR_UNSUPPORTED
+    # the combine writes the optional LSE; a negative stride is rejected before launch
+    p = _params(lse=0x30000, lse_stride_b=-1)
+    assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need, None) == \
+        _hip.FA_ERR_INVALID_ARGUMENT
+    assert "LSE" in lib.fa_last_error().decode()
     # split-K keeps the MFMA shapes: fp32 and other head dims go to the prefill entry point
     p = _params(dtype=_hip.F32, kv_dtype=_hip.F32)
     assert lib.fa_attention_splitk(ctypes.byref(p), 64, ctypes.c_void_p(0x40000), need, None) == _hip.FA_ERR_UNSUPPORTED
@@ -305,7 +308,7 @@ def test_paged_struct_layout(lib):
     ({}, {}, 100, _hip.FA_ERR_INVALID_ARGUMENT, "split_len"),
     ({}, dict(kv_dtype=_hip.FP8_E4M3, k_scale=0x50000, v_scale=0x50000), 128, _hip.FA_ERR_INVALID_ARGUMENT,
      "k/v dtype"),
-    ({}, dict(lse=0x30000), 128, _hip.FA_ERR_UNSUPPORTED, "LSE"),
+    ({}, dict(lse=0x30000, lse_stride_h=-1), 128, _hip.FA_ERR_INVALID_ARGUMENT, "LSE"),
     ({}, dict(dtype=_hip.F32, kv_dtype=_hip.F32), 128, _hip.FA_ERR_UNSUPPORTED, "dtype"),
     ({}, dict(head_dim=32, q_stride_b=4 * 16 * 32, q_stride_h=16 * 32, q_stride_n=32), 128, _hip.FA_ERR_UNSUPPORTED,
      "head_dim"),

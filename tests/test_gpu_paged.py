@@ -128,3 +128,22 @@ def test_paged_decode_cache_size():
         dense = fused_attn.attention_splitk(q, k, v, split_len=sk)
         paged = fused_attn.attention_paged(q, kc, vc, bt, sl, max_seqlen_k=32768, split_len=sk)
         assert torch.equal(dense, paged), sk
+
+
+def test_paged_lse_matches_dense_splitk_and_oracle():
+    """The combine's LSE from a paged pool equals the dense split-K kernel's bit for bit (same partials) and
+    the oracle's on the gathered keys; the zero-length sequence reports -inf."""
+    announce("paged lse")
+    lens = [300, 0, 1000, 64]
+    q, k, v, kc, vc, bt, sl = _dense_and_paged(4, 8, 2, 4, 1000, 128, 64, torch.bfloat16, lens=lens)
+    out, lse = fused_attn.attention_paged(q, kc, vc, bt, sl, causal=True, max_seqlen_k=1000, split_len=128,
+                                          return_lse=True)
+    assert torch.all(torch.isneginf(lse[1]))
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        ks, vs = k[b:b + 1, :, :n].contiguous(), v[b:b + 1, :, :n].contiguous()
+        dense, dlse = fused_attn.attention_splitk(q[b:b + 1], ks, vs, causal=True, split_len=128, return_lse=True)
+        assert torch.equal(dense, out[b:b + 1]) and torch.equal(dlse, lse[b:b + 1]), b
+        ref = orc.lse(q[b:b + 1].cpu(), ks.cpu(), causal=True).to(lse.device)
+        assert (lse[b:b + 1] - ref).abs().max().item() < 2.0 ** -8

@@ -87,7 +87,7 @@ def test_workspace_too_small_is_an_error():
     k = randn(1, 2, 512, 64, dtype=torch.bfloat16)
     ws = torch.empty(4, dtype=torch.float32, device="cuda")
     need = _hip.workspace_bytes(1, 4, 1, 64, 4)
-    assert need == 1 * 4 * 1 * 4 * (64 * 2 + 8)  # 16-bit partials + fp32 (max, sum) pairs
+    assert need == 1 * 4 * 1 * 4 * (64 * 4 + 8)  # fp32 partials + fp32 (max, sum) pairs
     out = _hip.splitk(q, k, k, split_len=128, workspace=ws)  # too small -> the wrapper allocates its own
     assert max_err(out, orc.attention(q.cpu(), k.cpu(), k.cpu())) <= TOL[torch.bfloat16]
 
@@ -149,3 +149,53 @@ def test_long_context_decode(split_len):
     err = max_err(out, ref)
     print(f"max_abs_err={err:.3e}", flush=True)
     assert err <= TOL[torch.bfloat16]
+
+
+def test_peaked_softmax_precision_splitk_vs_prefill():
+    """The seed-1478 peaked case (|scale| 0.3: each row follows a few V rows of magnitude ~4) through the
+    prefill kernel and split-K at two partition sizes, each against the fp32 oracle.  Split-K partials are
+    fp32 (the reference's format, triton_splitk.py:156-158), so split-K adds no 16-bit rounding to the
+    prefill kernel's: both meet the absolute bf16 bar, and split-K's error stays within the prefill
+    kernel's plus a bf16-output-rounding margin."""
+    gen = torch.Generator(device="cuda").manual_seed(1478)
+    q = randn(2, 64, 982, 128, dtype=torch.bfloat16, gen=gen)
+    k = randn(2, 8, 790, 128, dtype=torch.bfloat16, gen=gen)
+    v = randn(2, 8, 790, 128, dtype=torch.bfloat16, gen=gen)
+    for scale in (0.3, -0.3):
+        announce(f"peaked precision scale={scale}")
+        ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), scale=scale)
+        e_pre = max_err(fused_attn.attention(q, k, v, scale=scale), ref)
+        e64 = max_err(fused_attn.attention_splitk(q, k, v, scale=scale, split_len=64), ref)
+        e512 = max_err(fused_attn.attention_splitk(q, k, v, scale=scale, split_len=512), ref)
+        print(f"scale={scale}: max_abs_err prefill {e_pre:.4e}, split-K 64 {e64:.4e}, split-K 512 {e512:.4e}",
+              flush=True)
+        assert e_pre <= TOL[torch.bfloat16]
+        for e in (e64, e512):
+            assert e <= TOL[torch.bfloat16]
+            assert e <= e_pre + 2.0 ** -6  # within half a bf16 step at |o| ~ 4 of the prefill kernel's error
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k,d,split_len",
+                         [(2, 8, 2, 1, 3000, 128, 128), (1, 4, 1, 16, 2500, 64, 256), (2, 8, 2, 16, 8, 128, 64),
+                          (1, 4, 2, 4, 1300, 256, 512)])
+def test_splitk_lse_matches_oracle(b, h_q, h_kv, n_q, n_k, d, split_len, causal):
+    """The combine's natural-log LSE [B, Hq, Nq] (the reference's WRITE_LSE quantity, triton_fwd.py:169-172);
+    n_k < n_q causal rows see no key and report -inf."""
+    announce(f"splitk lse b={b} hq={h_q} nq={n_q} nk={n_k} d={d} split={split_len} causal={causal}")
+    torch.manual_seed(3)
+    q = randn(b, h_q, n_q, d, dtype=torch.bfloat16)
+    k = randn(b, h_kv, n_k, d, dtype=torch.bfloat16)
+    v = randn(b, h_kv, n_k, d, dtype=torch.bfloat16)
+    out, lse = fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split_len, return_lse=True)
+    ref = orc.lse(q.cpu(), k.cpu(), causal=causal).to(lse.device)
+    assert lse.shape == (b, h_q, n_q) and lse.dtype == torch.float32
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(lse))
+    # l sums the bf16-rounded P that the MFMA consumes: bf16-level relative error in l
+    assert (lse[fin] - ref[fin]).abs().max().item() < 2.0 ** -8
+    assert max_err(out, orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal)) <= TOL[torch.bfloat16]
+    # the LSE does not depend on the partitioning
+    _, lse1 = fused_attn.attention_splitk(q, k, v, causal=causal, split_len=max(64, -(-n_k // 64) * 64),
+                                          return_lse=True)
+    assert (lse1[fin] - lse[fin]).abs().max().item() < 2.0 ** -8

@@ -169,3 +169,49 @@ def test_attention_triton_alias_gives_the_kernel_result():
     kp, cuk, mk = fused_attn.pack_varlen([randn(n, 2, 128, dtype=torch.bfloat16) for n in (3, 50)])
     assert torch.equal(attention_varlen_triton(qp, kp, kp, cu, cuk, mx, mk, causal=True),
                        fused_attn.attention_varlen(qp, kp, kp, cu, cuk, mx, mk, causal=True))
+
+
+def _bench_lengths():
+    lens = torch.randint(0, 4097, (16,), generator=torch.Generator().manual_seed(0)).tolist()
+    lens[0], lens[1] = 0, 1
+    return lens
+
+
+@pytest.mark.parametrize("case", ["bench16", "ragged", "cross"])
+def test_varlen_rows_are_bit_identical_to_dense_calls(case):
+    """cu_seqlens indexing is exact: every sequence's rows of attention_varlen, and of its LSE, equal a dense
+    attention call on that sequence alone, bit for bit.  The varlen kernel runs 4-wave (128-row) blocks, as
+    the dense kernel does below 4096 queries, so each row goes through the same tile sequence; only the
+    workgroup schedule and the addressing differ.  Sequences of 0 and 1 tokens included."""
+    announce(f"varlen bit-exact {case}")
+    if case == "bench16":
+        lq = lk = [n for n in _bench_lengths()]
+        hq, hkv = 32, 8
+    elif case == "ragged":
+        lq = lk = [0, 1, 31, 32, 33, 127, 128, 129, 200, 1]
+        hq, hkv = 8, 2
+    else:  # chunked prefill against a cache: q shorter than k, causal alignment bottom-right
+        lq, lk = [8, 1, 0, 100, 129], [40, 1, 7, 100, 300]
+        hq, hkv = 8, 2
+    if case == "bench16":  # dense calls stay below 4096 queries (the 4-wave dense kernel)
+        lq = lk = [min(n, 4095) for n in lq]
+    d = 128
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    qs = [randn(n, hq, d, dtype=torch.bfloat16, gen=gen) for n in lq]
+    ks = [randn(n, hkv, d, dtype=torch.bfloat16, gen=gen) for n in lk]
+    vs = [randn(n, hkv, d, dtype=torch.bfloat16, gen=gen) for n in lk]
+    q, cu_q, max_q = fused_attn.pack_varlen(qs)
+    k, cu_k, max_k = fused_attn.pack_varlen(ks)
+    v, _, _ = fused_attn.pack_varlen(vs)
+    for causal in (True, False):
+        out, lse = _hip.varlen_fwd(q, k, v, cu_q, cu_k, max_q, max_k, causal=causal, return_lse=True)
+        for i, (nq, nk) in enumerate(zip(lq, lk)):
+            if nq == 0:
+                continue
+            qd = qs[i].transpose(0, 1)[None].contiguous()
+            kd = ks[i].transpose(0, 1)[None].contiguous()
+            vd = vs[i].transpose(0, 1)[None].contiguous()
+            od, ld = _hip.fwd(qd, kd, vd, causal=causal, return_lse=True)
+            s, e = int(cu_q[i]), int(cu_q[i + 1])
+            assert torch.equal(out[s:e], od[0].transpose(0, 1)), (case, i, causal)
+            assert torch.equal(lse[:, s:e], ld[0]), (case, i, causal)

@@ -70,6 +70,32 @@ def test_closed_forms():
     assert torch.all(outz[0, 0, :3] == 0) and torch.all(outz[0, 0, 3:].abs() > 0)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 4, 1, 37, 90, 16), (1, 2, 2, 9, 4, 8), (2, 4, 2, 13, 13, 32)])
+def test_lse_matches_float64_bruteforce(shape, causal):
+    b, hq, hkv, nq, nk, d = shape
+    torch.manual_seed(5)
+    q, k = torch.randn(b, hq, nq, d), torch.randn(b, hkv, nk, d)
+    ref = orc.lse_f64(q, k, causal=causal, scale=0.3)
+    got = orc.lse(q, k, causal=causal, scale=0.3).numpy()
+    assert np.array_equal(np.isfinite(ref), np.isfinite(got))  # (9, 4) causal: 5 rows see no key
+    fin = np.isfinite(ref)
+    np.testing.assert_allclose(got[fin], ref[fin], atol=2e-6, rtol=1e-6)
+    if causal and nq > nk:
+        assert np.all(got[..., : nq - nk] == -np.inf)
+
+
+def test_lse_closed_forms():
+    torch.manual_seed(6)
+    q, k = torch.randn(1, 1, 6, 8), torch.randn(1, 1, 6, 8)
+    lse = orc.lse(q, k, causal=True, scale=0.5)
+    # the first causal row sees only key 0: the LSE is its scaled score
+    torch.testing.assert_close(lse[0, 0, 0], (q[0, 0, 0] @ k[0, 0, 0]) * 0.5)
+    # zero queries: row i sees i + 1 equal (zero) scores -> ln(i + 1)
+    lse0 = orc.lse(torch.zeros_like(q), k, causal=True)
+    torch.testing.assert_close(lse0[0, 0], torch.log(torch.arange(1, 7, dtype=torch.float32)))
+
+
 def test_chunked_equals_whole():
     torch.manual_seed(4)
     q, k, v = torch.randn(2, 8, 70, 32), torch.randn(2, 2, 90, 32), torch.randn(2, 2, 90, 32)

@@ -51,6 +51,9 @@ COMBINE_CAUSAL = (pins.test_splitk_combine_is_exact, dict(causal=True, split_len
 SPLITS_KAT = (pins.test_choose_num_splits_known_answers, {})
 SPLIT_LEN = (pins.test_split_len_alignment, {})
 PAGED = (pins.test_paged_oracle_equals_dense_attention_on_the_scattered_keys, dict(causal=True))
+LSE_BRUTE = (pins.test_lse_matches_float64_bruteforce, dict(shape=(1, 2, 2, 9, 4, 8), causal=True))
+LSE_BRUTE_GQA = (pins.test_lse_matches_float64_bruteforce, dict(shape=(2, 4, 2, 13, 13, 32), causal=False))
+LSE_CLOSED = (pins.test_lse_closed_forms, {})
 PAGED_OOB = (pins.test_paged_oracle_out_of_pool_pages_read_as_zero_keys, {})
 
 MUTANTS = {
@@ -68,6 +71,13 @@ MUTANTS = {
                                 [SDPA_NONCAUSAL, BRUTE_GQA]),
     "empty_rows_left_nan": ("attention", "torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)",
                             "torch.softmax(s, dim=-1)", [MORE_Q_THAN_K, CLOSED]),
+    # natural-log LSE of the scores (triton_fwd.py:169-172)
+    "lse_scale_dropped": ("lse", "kf.transpose(-1, -2)) * scale", "kf.transpose(-1, -2))",
+                          [LSE_BRUTE_GQA, LSE_CLOSED]),
+    "lse_base_2": ("lse", "torch.logsumexp(s, dim=-1)", "torch.logsumexp(s, dim=-1) / math.log(2.0)",
+                   [LSE_BRUTE_GQA, LSE_CLOSED]),
+    "lse_top_left_mask": ("lse", "~causal_mask(n_q, n_k, device=s.device)", "~causal_mask(n_q, n_q, device=s.device)[:, :n_k]",
+                          [LSE_BRUTE]),
     # GQA head mapping (reference.py:16-21): q-head h reads kv-head h // g, not h % Hkv
     "gqa_heads_modulo": ("expand_kv", "torch.repeat_interleave(x, n_rep, dim=1)", "x.repeat(1, n_rep, 1, 1)",
                          [GQA, BRUTE_GQA]),
