@@ -19,7 +19,16 @@ before timing starts.  Printed as ONE JSON line:
   against 8 TB/s.  Also the n_q=16 causal spec-decode shape and the FP8 KV
   cache (B=16, Hq=64, Hkv=8, n_k=65536).
 * ``cpu_baseline``: the unfused fp32 oracle on the host cores, timed over the
-  whole prefill workload one (batch, kv-head group) slice at a time.
+  whole prefill workload one (batch, kv-head group) slice at a time; ``cpu_config0``
+  times it in full on the reference's CPU configuration (fp32 B=2 H=4 N=256 D=64
+  causal, 2 warm-up + 3 timed calls, benchmarks/bench.py:54-61 in the reference).
+* ``max_abs_err`` beside every timed attention workload: against the unfused fp32
+  reference backend (fused_attn/reference.py) on one (batch, kv-head group) slice of
+  the timed call's output, as the reference's benchmark records it
+  (benchmarks/bench.py:87,110-114).
+* ``context``: torch's scaled_dot_product_attention on the same GPU and workload
+  (flash or memory-efficient backend), and the single-pass prefill kernel on the
+  decode shape (benchmarks/bench_decode.py:41-65 in the reference).
 """
 from __future__ import annotations
 
@@ -81,6 +90,26 @@ def _time_calls(fn, steps, warmup):
     return wall, ev
 
 
+def _ref_err(out, q, k, v, causal, scale=None):
+    """max |out - ref| against the unfused fp32 reference backend (fused_attn/reference.py) on the same
+    inputs (the reference benchmark's max_abs_err, benchmarks/bench.py:87,110-114)."""
+    from fused_attn.reference import attention_reference
+
+    ref = attention_reference(q.float(), k.float(), v.float(), causal=causal, scale=scale)
+    return round((out.float() - ref).abs().max().item(), 6)
+
+
+def _slice_err(out, q, k, v, causal):
+    """_ref_err on the first (batch, kv-head group) slice of a [B, H, N, D] call."""
+    g = q.shape[1] // k.shape[1]
+    return _ref_err(out[:1, :g], q[:1, :g], k[:1, :1], v[:1, :1], causal)
+
+
+def _batch0_err(out, q, k, v, causal):
+    """_ref_err on batch element 0 of a [B, H, N, D] call (every head)."""
+    return _ref_err(out[:1], q[:1], k[:1], v[:1], causal)
+
+
 def _traffic_bytes():
     try:
         text = open(TRAFFIC_FILE).read()
@@ -90,21 +119,68 @@ def _traffic_bytes():
     return float(m.group(1)) if m else None
 
 
-def bench_prefill(steps, warmup):
+PREFILL_SETS = 3  # input sets the timed prefill calls rotate through (3 x 335.5 MB > the 256 MiB MALL)
+
+
+def bench_prefill(steps, warmup, with_sdpa=True):
+    """The headline prefill workload; calls rotate through PREFILL_SETS input sets so that no call
+    finds its inputs left in the memory-side cache by the previous one."""
     import torch
 
     import fused_attn
 
     c = PREFILL
     g = torch.Generator(device="cuda").manual_seed(0)
-    q = torch.randn(c["b"], c["hq"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
-    k = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
-    v = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
+    sets = []
+    for _ in range(PREFILL_SETS):
+        q = torch.randn(c["b"], c["hq"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
+        k = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
+        v = torch.randn(c["b"], c["hkv"], c["n"], c["d"], device="cuda", generator=g).bfloat16()
+        sets.append((q, k, v))
+    q, k, v = sets[0]
     out = fused_attn.attention(q, k, v, causal=True)
-    assert not torch.isnan(out).any()
-    wall, ev = _time_calls(lambda: fused_attn.attention(q, k, v, causal=True), steps, warmup)
+    err = _slice_err(out, q, k, v, True)
+    del out
+    turn = [0]
+
+    def step():
+        q, k, v = sets[turn[0] % PREFILL_SETS]
+        turn[0] += 1
+        return fused_attn.attention(q, k, v, causal=True)
+
+    wall, ev = _time_calls(step, steps, warmup)
     flops = attn_flops(c["b"], c["hq"], c["n"], c["d"], True)
-    return flops, wall, ev
+    sdpa = bench_sdpa(sets[0], steps, warmup, flops) if with_sdpa else None
+    del sets
+    torch.cuda.empty_cache()
+    return flops, wall, ev, err, sdpa
+
+
+def bench_sdpa(qkv, steps, warmup, flops):
+    """Context: torch's scaled_dot_product_attention on the same workload and GPU (the reference benchmark's
+    torch.sdpa line, benchmarks/bench.py:94-96), restricted to its flash and memory-efficient backends;
+    GQA through enable_gqa.  None when neither backend takes the call."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    q, k, v = qkv
+    for be in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel(be):
+                fn = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)  # noqa: E731
+                out = fn()
+                err = _slice_err(out, q, k, v, True)
+                del out
+                wall, ev = _time_calls(fn, steps, warmup)
+        except RuntimeError as e:
+            last = f"{type(e).__name__}: {str(e)[:120]}"
+            continue
+        return {"workload": "torch.nn.functional.scaled_dot_product_attention, same prefill workload (context)",
+                "backend": str(be).split(".")[-1], "ms": round(wall * 1e3, 4), "ms_events": round(ev * 1e3, 4),
+                "TFLOP_s": round(flops / wall / 1e12, 1), "TFLOP_s_events": round(flops / ev / 1e12, 1),
+                "max_abs_err": err}
+    return {"workload": "torch sdpa", "skipped": last}
 
 
 def bench_prefill_extras(steps, warmup):
@@ -116,14 +192,15 @@ def bench_prefill_extras(steps, warmup):
     res = {}
     g = torch.Generator(device="cuda").manual_seed(0)
 
-    def entry(name, workload, fn, flops):
+    def entry(name, workload, fn, flops, err_fn=None):
         out = fn()
-        assert not torch.isnan(out).any()
+        err = err_fn(out) if err_fn is not None else _slice_err(out, q, k, v, True)
+        del out
         wall, ev = _time_calls(fn, steps, warmup)
         res[name] = {"workload": workload, "ms": round(wall * 1e3, 4), "ms_events": round(ev * 1e3, 4),
                      "TFLOP_s": round(flops / wall / 1e12, 1),
                      "TFLOP_s_events": round(flops / ev / 1e12, 1),
-                     "mfma_frac": round(flops / ev / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+                     "mfma_frac": round(flops / ev / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4), "max_abs_err": err}
 
     q = torch.randn(4, 16, 4096, 64, device="cuda", generator=g).bfloat16()
     k = torch.randn(4, 16, 4096, 64, device="cuda", generator=g).bfloat16()
@@ -166,10 +243,18 @@ def bench_prefill_extras(steps, warmup):
     v = torch.randn(total, 8, 128, device="cuda", generator=g).bfloat16()
     cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
     mx = max(lens)
+    def varlen_err(out):  # the two longest sequences, per sequence against the reference backend
+        errs = []
+        for i in sorted(range(len(lens)), key=lambda i: -lens[i])[:2]:
+            s, e = int(cu[i]), int(cu[i + 1])
+            seq = [x[s:e].transpose(0, 1)[None] for x in (q, k, v)]
+            errs.append(_ref_err(out[s:e].transpose(0, 1)[None], *seq, True))
+        return max(errs)
+
     entry("varlen_prefill", f"varlen causal prefill, 16 sequences (lengths U[0,4096] by seed 0, one 0, one 1; "
           f"{total} tokens) Hq=32 Hkv=8 D=128 bf16",
           lambda: fused_attn.attention_varlen(q, k, v, cu, cu, mx, mx, causal=True),
-          sum(attn_flops(1, 32, n, 128, True) for n in lens))
+          sum(attn_flops(1, 32, n, 128, True) for n in lens), err_fn=varlen_err)
     return res
 
 
@@ -187,6 +272,7 @@ def bench_decode(steps, warmup, only_128=False):
     for nq, causal, split in cases:
         q = torch.randn(c["b"], c["hq"], nq, c["d"], device="cuda", generator=g).bfloat16()
         fn = lambda: fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split)  # noqa: E731
+        err = _batch0_err(fn(), q, k, v, causal)
         wall, ev = _time_calls(fn, steps, warmup)
         nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
         key = ("decode" if nq == 1 else "spec_decode_nq16") + ("" if split else "_default_split")
@@ -197,10 +283,24 @@ def bench_decode(steps, warmup, only_128=False):
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
     if only_128:
         return res
+    # context: the single-pass prefill kernel on the n_q = 1 decode shape (the reference's bench_decode
+    # prints single-pass beside split-K and FP8 per context length, benchmarks/bench_decode.py:41-65)
+    q = torch.randn(c["b"], c["hq"], 1, c["d"], device="cuda", generator=g).bfloat16()
+    fn = lambda: fused_attn._hip.fwd(q, k, v)  # noqa: E731
+    err = _batch0_err(fn(), q, k, v, False)
+    wall, ev = _time_calls(fn, max(3, steps // 4), warmup)
+    nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
+    res["single_pass_decode"] = {
+        "workload": f"single-pass prefill kernel on the decode shape B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 "
+                    f"n_k={c['nk']} D={c['d']} bf16 (context: no key split)",
+        "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+        "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
+    }
     res.update(bench_paged(k, v, steps, warmup, g))
     del k, v
     torch.cuda.empty_cache()
@@ -209,8 +309,12 @@ def bench_decode(steps, warmup, only_128=False):
     k8, ks = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
     v8, vs = fused_attn.quantize_kv_fp8(torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g))
     torch.cuda.empty_cache()
+    from fused_attn.fp8 import dequantize_kv_fp8
+
+    kd0, vd0 = dequantize_kv_fp8(k8[:1], ks[:1]), dequantize_kv_fp8(v8[:1], vs[:1])
     for split in (128, None):
         fn = lambda: fused_attn.attention_fp8(q, k8, ks, v8, vs, split_len=split)  # noqa: E731
+        err = _ref_err(fn()[:1], q[:1], kd0, vd0, False)  # against the reference on the dequantised cache
         wall, ev = _time_calls(fn, steps, warmup)
         nbytes = 2 * k8.numel() + 2 * ks.numel() * 4 + 2 * q.numel() * 2
         keys = split or fused_attn.ops.default_split_len(1, c["nk"], c["b"], c["hkv"], c["hq"] // c["hkv"])
@@ -220,9 +324,9 @@ def bench_decode(steps, warmup, only_128=False):
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
-    del q, k8, ks, v8, vs
+    del q, k8, ks, v8, vs, kd0, vd0
     torch.cuda.empty_cache()
     res.update(bench_decode_d256(steps, warmup, g))
     return res
@@ -239,9 +343,10 @@ def bench_decode_d256(steps, warmup, g):
     v = torch.randn(b, hkv, nk, d, device="cuda", generator=g).bfloat16()
     q = torch.randn(b, hq, 1, d, device="cuda", generator=g).bfloat16()
     fn = lambda: fused_attn.attention_splitk(q, k, v, split_len=128)  # noqa: E731
+    err = _batch0_err(fn(), q, k, v, False)
     wall, ev = _time_calls(fn, steps, warmup)
     nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
-    res = {"decode_d256": {
+    res = {"decode_d256": {"max_abs_err": err,
         "workload": f"split-K B={b} Hq={hq} Hkv={hkv} n_q=1 n_k={nk} D={d} bf16, 128-key partitions + LSE combine",
         "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
         "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
@@ -265,6 +370,7 @@ def bench_paged(k, v, steps, warmup, g, page_size=64):
     for split in (128, None):
         keys = split or fused_attn.ops.default_split_len(1, c["nk"], c["b"], c["hkv"], c["hq"] // c["hkv"])
         fn = lambda: fused_attn.attention_paged(q, kc, vc, bt, sl, max_seqlen_k=c["nk"], split_len=keys)  # noqa: E731
+        err = _batch0_err(fn(), q, k, v, False)  # the pool holds the dense K/V, shuffled into pages
         wall, ev = _time_calls(fn, steps, warmup)
         nbytes = 2 * kc.numel() * 2 + 2 * q.numel() * 2 + bt.numel() * 4
         res["paged_decode" + ("" if split else "_default_split")] = {
@@ -273,7 +379,7 @@ def bench_paged(k, v, steps, warmup, g, page_size=64):
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
     return res
 
@@ -287,6 +393,14 @@ def bench_quantize(steps, warmup):
     c = FP8_DECODE
     g = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(c["b"], c["hkv"], c["nk"], c["d"], device="cuda", generator=g).bfloat16()
+    # correctness beside the timing: bytes and scales of batch element 0 against the reference's torch chain
+    from fused_attn.fp8 import _quantize_kv_fp8_torch
+
+    x8, sc = fused_attn.quantize_kv_fp8(x)
+    r8, rs = _quantize_kv_fp8_torch(x[:1])
+    mismatches = int((x8[:1].view(torch.uint8) != r8.view(torch.uint8)).sum().item()) + \
+        int((sc[:1] != rs).sum().item())
+    del x8, sc, r8, rs
     wall, ev = _time_calls(lambda: fused_attn.quantize_kv_fp8(x), steps, warmup)
     nblk = -(-c["nk"] // 64)
     nbytes = x.numel() * 2 + x.numel() + c["b"] * c["hkv"] * nblk * 4
@@ -297,7 +411,33 @@ def bench_quantize(steps, warmup):
         "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
         "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
         "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+        "mismatches_vs_torch_chain": mismatches,
     }
+
+
+def cpu_config0():
+    """The reference's CPU configuration in full: dense causal MHA fp32 B=2 Hq=Hkv=4 n_q=n_k=256 D=64,
+    q/k/v ~ N(0,1) from torch.manual_seed(0), through the fp32 oracle on the host cores; 2 warm-up and 3
+    timed calls, as the reference times its CPU path (benchmarks/bench.py:54-61)."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import attention_oracle as orc
+
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(2, 4, 256, 64) for _ in range(3))
+    for _ in range(2):
+        orc.attention(q, k, v, causal=True)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        orc.attention(q, k, v, causal=True)
+    dt = (time.perf_counter() - t0) / 3
+    flops = attn_flops(2, 4, 256, 64, True)
+    return {"workload": "causal MHA fp32 B=2 Hq=Hkv=4 n_q=n_k=256 D=64 (the reference's CPU configuration), "
+                        "unfused fp32 oracle, 2 warm-up + 3 timed calls",
+            "ms": round(dt * 1e3, 4), "TFLOP_s": round(flops / dt / 1e12, 6), "cores": torch.get_num_threads(),
+            "kind": "port"}
 
 
 def cpu_baseline(passes=3):
@@ -344,7 +484,7 @@ def copy_calibration(steps, warmup, nbytes=1 << 30):
 
 def run_only(which, steps, warmup):
     if which == "prefill":
-        flops, wall, ev = bench_prefill(steps, warmup)
+        flops, wall, ev, _, _ = bench_prefill(steps, warmup, with_sdpa=False)
         print(f"prefill: {flops / ev / 1e12:.1f} TFLOP/s kernel, {ev * 1e3:.4f} ms", flush=True)
     elif which == "quantize":
         print(json.dumps(bench_quantize(steps, warmup)), flush=True)
@@ -377,7 +517,7 @@ def main():
     if a.only is not None:
         run_only(a.only, a.steps, a.warmup)
         return
-    flops, wall, ev = bench_prefill(a.steps, a.warmup)
+    flops, wall, ev, err, sdpa = bench_prefill(a.steps, a.warmup)
     achieved = flops / ev / 1e12
     c = PREFILL
     line = {
@@ -393,7 +533,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: q/k/v ~ N(0,1) from a seeded generator, cast to bf16, resident in HBM",
+        "data": f"synthetic: q/k/v ~ N(0,1) from a seeded generator, cast to bf16, resident in HBM; the timed "
+                f"calls rotate through {PREFILL_SETS} input sets",
+        "max_abs_err": err,
         "config": {"workload": f"causal GQA prefill B={c['b']} Hq={c['hq']} Hkv={c['hkv']} N={c['n']} D={c['d']} "
                                "bf16 [B,H,N,D]", "batch": c["b"], "heads_q": c["hq"], "heads_kv": c["hkv"],
                    "seq_len": c["n"], "head_dim": c["d"], "causal": True, "parallelism": "single-gpu"},
@@ -402,12 +544,14 @@ def main():
                      "traffic": _traffic_bytes(), "kernel": "attn_fwd_kernel<128,BF16,8>",
                      "kernel_ms": round(ev * 1e3, 4)},
     }
+    line["context"] = {"sdpa": sdpa}
     line["prefill_other"] = bench_prefill_extras(max(5, a.steps // 2), max(2, a.warmup))
     if not a.no_decode:
         line["decode"] = bench_decode(max(5, a.steps), max(2, a.warmup))
         line["quantize"] = bench_quantize(max(5, a.steps), max(2, a.warmup))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        line["cpu_config0"] = cpu_config0()
     print(json.dumps(line), flush=True)
 
 
