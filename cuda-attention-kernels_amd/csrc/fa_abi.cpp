@@ -13,6 +13,8 @@
 #include "../../include/fused_attn_hip.h"
 #include "fa_internal.hpp"
 
+static_assert(FA_SPLITK_NOALLOC_MAX_BYTES == fa::kSplitkScratchBytes, "header limit and scratch array size differ");
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -155,6 +157,36 @@ fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* w
     return fail(FA_ERR_INVALID_ARGUMENT, "negative FP8 scale stride");
   const char* err = nullptr;
   st = fa::run_splitk(*p, split_len, workspace, reinterpret_cast<hipStream_t>(stream), &err);
+  if (st != FA_OK) return fail(st, err ? err : "launch failed");
+  return FA_OK;
+}
+
+fa_status fa_attention_splitk_noalloc(const fa_fwd_params* p, int32_t split_len, void* stream) {
+  g_last_error.clear();
+  fa_status st = validate(p, /*varlen=*/false, /*fp8_ok=*/true, /*generic_ok=*/false);
+  if (st != FA_OK) return st;
+  if (p->lse != nullptr && (p->lse_stride_b < 0 || p->lse_stride_h < 0))
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
+  if (split_len <= 0 || split_len % 64 != 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "split_len must be a positive multiple of 64");
+  if (p->batch == 0 || p->seqlen_q == 0) return FA_OK;
+  if (p->kv_dtype == FA_DTYPE_FP8_E4M3 && (p->scale_stride_b < 0 || p->scale_stride_h < 0))
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative FP8 scale stride");
+  const int32_t splits = p->seqlen_k > 0 ? (p->seqlen_k + split_len - 1) / split_len : 1;
+  const size_t need = fa_splitk_workspace_bytes(p->batch, p->heads_q, p->seqlen_q, p->head_dim, splits);
+  if (need > fa::kSplitkScratchBytes) {
+    char buf[200];
+    snprintf(buf, sizeof(buf),
+             "split-K needs %zu bytes of workspace here; the no-allocation entry point holds at most %zu "
+             "(use longer partitions, or fa_attention_splitk with a caller workspace)",
+             need, fa::kSplitkScratchBytes);
+    return fail(FA_ERR_WORKSPACE, buf);
+  }
+  const char* err = nullptr;
+  void* scratch = nullptr;
+  st = fa::splitk_scratch(&scratch, &err);
+  if (st != FA_OK) return fail(st, err ? err : "scratch lookup failed");
+  st = fa::run_splitk(*p, split_len, scratch, reinterpret_cast<hipStream_t>(stream), &err);
   if (st != FA_OK) return fail(st, err ? err : "launch failed");
   return FA_OK;
 }

@@ -82,6 +82,10 @@ fa_status run_fwd_generic(const fa_fwd_params& p, bool varlen, hipStream_t strea
 // fp32 at head dims 32 to 256 on the fp32 MFMA (fa_prefill_f32.hip); run_fwd forwards those here.
 fa_status run_fwd_f32(const fa_fwd_params& p, bool varlen, hipStream_t stream, const char** err);
 fa_status run_quantize_fp8(const fa_quant_params& p, hipStream_t stream, const char** err);
+// Largest workspace the no-allocation split-K entry point holds (a static device array per GPU).
+constexpr size_t kSplitkScratchBytes = size_t{64} << 20;
+// This device's address of that array (looked up once per device), for fa_attention_splitk_noalloc.
+fa_status splitk_scratch(void** ptr, const char** err);
 // kv: paged K/V (nullptr for a dense cache)
 fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,
                      const char** err, const fa_paged_kv* kv = nullptr);

@@ -45,6 +45,7 @@
 #include <float.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "fa_device.hpp"
@@ -766,6 +767,39 @@ template <int D, class E>
 static hipError_t launch_split(const TileArgs& a, bool fp8, bool paged, int nw, hipStream_t stream) {
   if (paged) return launch_split_nw<D, E, E, true>(a, nw, stream);
   return fp8 ? launch_split_nw<D, E, FP8, false>(a, nw, stream) : launch_split_nw<D, E, E, false>(a, nw, stream);
+}
+
+// ------------------------------------------------------------------------------------
+// Scratch for the entry point that allocates nothing (fa_attention_splitk_noalloc): the
+// split-K workspace lives in a file-scope device array, one copy per GPU for the life of the
+// process.  Host code may not use the array's name as a device address: each device's
+// address comes from hipGetSymbolAddress, called once per device with that device current.
+// ------------------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[kSplitkScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+fa_status splitk_scratch(void** ptr, const char** err) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, err);
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = "device index beyond the scratch table";
+    return FA_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, err);
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return FA_OK;
 }
 
 fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace, hipStream_t stream,

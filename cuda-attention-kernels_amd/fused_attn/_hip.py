@@ -140,6 +140,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.fa_splitk_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_attention_splitk.argtypes = [P, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.fa_attention_splitk.restype = ctypes.c_int
+    lib.fa_attention_splitk_noalloc.argtypes = [P, ctypes.c_int32, ctypes.c_void_p]
+    lib.fa_attention_splitk_noalloc.restype = ctypes.c_int
     lib.fa_choose_num_splits.argtypes = [ctypes.c_int32] * 5
     lib.fa_choose_num_splits.restype = ctypes.c_int32
     lib.fa_attention_paged_decode.argtypes = [P, ctypes.POINTER(PagedKV), ctypes.c_int32, ctypes.c_void_p,
@@ -468,6 +470,35 @@ def splitk(q, k, v, causal: bool = False, scale: Optional[float] = None, split_l
         _check(lib.fa_attention_splitk(ctypes.byref(p), int(split_len), ctypes.c_void_p(workspace.data_ptr()),
                                        workspace.numel() * workspace.element_size(),
                                        ctypes.c_void_p(_stream(q))), "attention_splitk")
+    return (o, lse) if return_lse else o
+
+
+SPLITK_NOALLOC_MAX_BYTES = 64 << 20  # FA_SPLITK_NOALLOC_MAX_BYTES
+
+
+def splitk_noalloc(q, k, v, causal: bool = False, scale: Optional[float] = None, split_len: int = 128,
+                   k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None, return_lse: bool = False):
+    """``splitk`` through fa_attention_splitk_noalloc: the library uses its own static per-GPU workspace
+    (at most SPLITK_NOALLOC_MAX_BYTES) and allocates nothing; calls overlapping on one GPU race.  ``out``
+    (and the LSE) are the caller's to provide for a call that must allocate nothing either."""
+    fp8 = _FP8 is not None and k.dtype == _FP8
+    _check_qkv(q, k, v, "dense", kv_fp8=fp8)
+    if fp8:
+        _check_fp8_scales(k, k_scale, v_scale)
+    _require_gpu(q, k, v)
+    lib = load_library()
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    q, k, v = _prep_qkv(q, k, v, kv_fp8=fp8)
+    if fp8:
+        k_scale, v_scale = _prep_fp8_scales(k, k_scale, v_scale)
+    o = _new_output(q) if out is None else out
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if return_lse else None
+    p = make_params(q, k, v, o, causal, scale, k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None,
+                    lse=lse)
+    with torch.cuda.device(q.device):
+        _check(lib.fa_attention_splitk_noalloc(ctypes.byref(p), int(split_len), ctypes.c_void_p(_stream(q))),
+               "attention_splitk_noalloc")
     return (o, lse) if return_lse else o
 
 

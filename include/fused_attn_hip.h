@@ -120,6 +120,18 @@ size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_
 fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* fa_attention_splitk without a caller workspace, for callers that cannot allocate device memory
+   (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+   counterpart in the reference.  Same arguments, validation, kernels and results as
+   fa_attention_splitk; the workspace is a static device array the library holds on each GPU for
+   the life of the process (FA_SPLITK_NOALLOC_MAX_BYTES), so a request whose
+   fa_splitk_workspace_bytes exceeds that size fails with FA_ERR_WORKSPACE.  The library calls no
+   allocation routine on this path.  Every call on a GPU uses that GPU's one array: calls that
+   overlap on one GPU (other streams, other threads) race and must be serialised by the caller.
+   No state in the array has to start at zero (each call writes every partial it reads). */
+#define FA_SPLITK_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+fa_status fa_attention_splitk_noalloc(const fa_fwd_params* p, int32_t split_len, void* stream);
+
 /* Paged (block-table) K/V for fa_attention_paged_decode.  The K and V pools hold
    num_pages pages of page_size keys; p->k / p->v point at the pools and
    p->k_stride_h / k_stride_n (v likewise) are the head and key strides inside a
