@@ -326,7 +326,25 @@ def bench_decode(steps, warmup, only_128=False):
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
             "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
-    del q, k8, ks, v8, vs, kd0, vd0
+    # the same FP8 cache scattered into a shuffled pool of 64-key pages with per-page block scales
+    kc, vc, ksp, vsp, bt, sl = fused_attn.paged_from_dense_fp8(k8, ks, v8, vs, 64,
+                                                               generator=torch.Generator().manual_seed(0))
+    for split in (128, None):
+        keys = split or fused_attn.ops.default_split_len(1, c["nk"], c["b"], c["hkv"], c["hq"] // c["hkv"])
+        fn = lambda: fused_attn.attention_paged(q, kc, vc, bt, sl, max_seqlen_k=c["nk"], split_len=keys,  # noqa: E731
+                                                k_scale=ksp, v_scale=vsp)
+        err = _ref_err(fn()[:1], q[:1], kd0, vd0, False)
+        wall, ev = _time_calls(fn, steps, warmup)
+        nbytes = 2 * kc.numel() + 2 * ksp.numel() * 4 + 2 * q.numel() * 2 + bt.numel() * 4
+        res["paged_fp8_decode" + ("" if split else "_default_split")] = {
+            "workload": f"paged FP8-KV split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 n_k={c['nk']} D={c['d']}, "
+                        f"64-key e4m3fn pages in shuffled order with per-page fp32 block scales, {keys}-key partitions"
+                        f"{'' if split else ' (default partition policy)'}",
+            "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
+            "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
+            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
+        }
+    del q, k8, ks, v8, vs, kd0, vd0, kc, vc, ksp, vsp
     torch.cuda.empty_cache()
     res.update(bench_decode_d256(steps, warmup, g))
     return res

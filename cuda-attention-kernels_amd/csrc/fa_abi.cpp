@@ -197,7 +197,7 @@ fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* k
   if (p == nullptr || kv == nullptr) return fail(FA_ERR_INVALID_ARGUMENT, "params is NULL");
   fa_fwd_params q = *p;
   q.k_stride_b = q.v_stride_b = 0;  // keys are found through the block table
-  fa_status st = validate(&q, /*varlen=*/false, /*fp8_ok=*/false, /*generic_ok=*/false);
+  fa_status st = validate(&q, /*varlen=*/false, /*fp8_ok=*/true, /*generic_ok=*/false);
   if (st != FA_OK) return st;
   if (q.lse != nullptr && (q.lse_stride_b < 0 || q.lse_stride_h < 0))
     return fail(FA_ERR_INVALID_ARGUMENT, "negative LSE stride");
@@ -205,6 +205,11 @@ fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* k
     return fail(FA_ERR_INVALID_ARGUMENT, "split_len must be a positive multiple of 64");
   if (kv->page_size <= 0 || kv->page_size % 32 != 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "page_size must be a positive multiple of 32");
+  const bool fp8 = q.kv_dtype == FA_DTYPE_FP8_E4M3;
+  if (fp8 && kv->page_size % 64 != 0)
+    return fail(FA_ERR_INVALID_ARGUMENT, "FP8 pools need page_size a multiple of 64 (64-key scale blocks)");
+  if (fp8 && (q.scale_stride_b < 0 || q.scale_stride_h < 0))
+    return fail(FA_ERR_INVALID_ARGUMENT, "negative FP8 scale stride");
   if (kv->num_pages < 0 || kv->block_table_cols < 0) return fail(FA_ERR_INVALID_ARGUMENT, "negative page count");
   if (q.batch == 0 || q.seqlen_q == 0) return FA_OK;
   if (kv->block_table == nullptr || kv->seqlens_k == nullptr)

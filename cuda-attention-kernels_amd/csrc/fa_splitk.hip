@@ -41,7 +41,10 @@
 // 256 entries in four VGPRs); each 32-key half of a tile lies inside one page (page
 // sizes are multiples of 32), so its buffer descriptor is built from one entry read
 // with v_readlane, and the DMA addressing inside the tile is unchanged.  An entry
-// outside [0, num_pages) gets an empty descriptor: its keys read as zeros.
+// outside [0, num_pages) gets an empty descriptor: its keys read as zeros.  FP8 pools carry
+// their block scales per page, [num_pages, Hkv, page_size / 64] (page sizes are then
+// multiples of 64, so a 64-key scale block lies inside one page); a page outside the pool
+// gets scale 0, so its keys stay zero keys.
 #include <float.h>
 
 #include <algorithm>
@@ -77,7 +80,6 @@ attn_splitk_kernel(const TileArgs a) {
   constexpr int QPW = (TILE_BYTES / 1024) / NW;
   static_assert(BN % 32 == 0 && D % 32 == 0 && (D == 64 || D == 128 || D == 256), "tile shape");
   static_assert(TILE_BYTES % (1024 * NW) == 0, "tile loads must split evenly over the waves");
-  static_assert(!(PAGED && IS_FP8), "paged K/V is 16-bit");
   constexpr int PG_REGS = 4;  // paged: block-table entries held per lane (64 * PG_REGS per workgroup)
   constexpr float NEG_INF = -__builtin_inff();
 
@@ -181,15 +183,19 @@ attn_splitk_kernel(const TileArgs a) {
   // weight is negligible beside the largest lose bits.
   float v_ref = 1.f;
   if (KV::bytes == 1) {
-    ksc = a.k_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
-    vsc = a.v_scale + (int64_t)b * a.ssb + (int64_t)kvh * a.ssh;
-    const int blo = klo / 64, bhi = khi > klo ? (khi + 63) / 64 : blo;
-    float vm = 0.f;
-    for (int bk = blo + (int)(threadIdx.x & 63); bk < bhi; bk += 64) vm = fmaxf(vm, vsc[bk]);
-    vm = max_xor32(vm);
+    // (paged: the scale pools' base for this kv-head; a block's scale is at page * ssb + its
+    // 64-key block inside the page)
+    ksc = a.k_scale + (PAGED ? 0 : (int64_t)b * a.ssb) + (int64_t)kvh * a.ssh;
+    vsc = a.v_scale + (PAGED ? 0 : (int64_t)b * a.ssb) + (int64_t)kvh * a.ssh;
+    if constexpr (!PAGED) {
+      const int blo = klo / 64, bhi = khi > klo ? (khi + 63) / 64 : blo;
+      float vm = 0.f;
+      for (int bk = blo + (int)(threadIdx.x & 63); bk < bhi; bk += 64) vm = fmaxf(vm, vsc[bk]);
+      vm = max_xor32(vm);
 #pragma unroll
-    for (int sh = 16; sh >= 1; sh >>= 1) vm = fmaxf(vm, __shfl_xor(vm, sh, 64));
-    v_ref = fmaxf(vm, FLT_MIN);
+      for (int sh = 16; sh >= 1; sh >>= 1) vm = fmaxf(vm, __shfl_xor(vm, sh, 64));
+      v_ref = fmaxf(vm, FLT_MIN);
+    }
   }
 
   // A negative softmax scale is applied by negating Q (exact for 16-bit floats),
@@ -221,6 +227,27 @@ attn_splitk_kernel(const TileArgs a) {
     for (int r = 0; r < PG_REGS; ++r) {
       const int sl = first_slot + 64 * r + (tid & 63);
       pg[r] = sl < slot_end ? bt[sl] : -1;
+    }
+    if constexpr (IS_FP8) {
+      // v_ref over the V block scales of keys [klo, khi): lane i looks at the pages its
+      // entries hold (slots first_slot + i + 64 r), page_size / 64 blocks each
+      const int bpp = a.page_size / 64;
+      float vm = 0.f;
+#pragma unroll
+      for (int r = 0; r < PG_REGS; ++r) {
+        const int sl = first_slot + 64 * r + (tid & 63);
+        const int page = pg[r];
+        if ((uint32_t)page < (uint32_t)a.num_pages) {
+          for (int wb = 0; wb < bpp; ++wb) {
+            const int key = (sl * bpp + wb) * 64;
+            if (key >= klo && key < khi) vm = fmaxf(vm, vsc[(int64_t)page * a.ssb + wb]);
+          }
+        }
+      }
+      vm = max_xor32(vm);
+#pragma unroll
+      for (int sh = 16; sh >= 1; sh >>= 1) vm = fmaxf(vm, __shfl_xor(vm, sh, 64));
+      v_ref = fmaxf(vm, FLT_MIN);
     }
   }
   // ---- Q fragments (B operand of S^T), resident for the whole kernel -------------
@@ -291,8 +318,10 @@ attn_splitk_kernel(const TileArgs a) {
         const int half = (blk * 1024 / (D * KV::bytes)) / 32;
         const __amdgpu_buffer_rsrc_t ck = (KB > 1 && half) ? rk[KB - 1] : rk[0];
         const __amdgpu_buffer_rsrc_t cv = (KB > 1 && half) ? rv[KB - 1] : rv[0];
-        if (do_k) lds_dma16<true>(ck, kl + blk * 1024, (kperm(r) - 32 * half) * (int)krow_bytes + ((p ^ Shape::swz_k(r)) * 16));
-        if (do_v) lds_dma16<true>(cv, vl + blk * 1024, (r - 32 * half) * (int)vrow_bytes + ((p ^ Shape::swz_v(r)) * 16));
+        const int sk = IS_FP8 ? Shape8::swz_k(r) : Shape::swz_k(r);
+        const int sv = IS_FP8 ? Shape8::swz_v(r) : Shape::swz_v(r);
+        if (do_k) lds_dma16<true>(ck, kl + blk * 1024, (kperm(r) - 32 * half) * (int)krow_bytes + ((p ^ sk) * 16));
+        if (do_v) lds_dma16<true>(cv, vl + blk * 1024, (r - 32 * half) * (int)vrow_bytes + ((p ^ sv) * 16));
       }
       return;
     }
@@ -425,9 +454,23 @@ attn_splitk_kernel(const TileArgs a) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       if constexpr (KV::bytes == 1) {
-        const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
-        sc[kb] = fmaxf(c_abs * ksc[blk], kMinScale);
-        vs[kb] = vsc[blk] / v_ref;
+        float ks, vsv;
+        if constexpr (PAGED) {
+          // the 64-key block of key n0 + 32 kb inside its page; keys at or past khi are
+          // masked and pages outside the pool hold zero keys: scale 0 for both
+          const int nk = n0 + kb * 32;
+          const int page = nk < khi ? page_of(nk) : -1;
+          const bool ok = (uint32_t)page < (uint32_t)a.num_pages;
+          const int64_t at = ok ? (int64_t)page * a.ssb + (nk % a.page_size) / 64 : 0;
+          ks = ok ? ksc[at] : 0.f;
+          vsv = ok ? vsc[at] : 0.f;
+        } else {
+          const int blk = (n0 + kb * 32) >> 6;  // 64-key FP8 scale block
+          ks = ksc[blk];
+          vsv = vsc[blk];
+        }
+        sc[kb] = fmaxf(c_abs * ks, kMinScale);
+        vs[kb] = vsv / v_ref;
       } else {
         sc[kb] = c_abs;
         vs[kb] = 1.f;
@@ -734,8 +777,9 @@ int splitk_waves_for_rows(int rows) { return rows <= 32 ? 1 : (rows <= 64 ? 2 : 
 // less memory work per instruction stream (FP8 tiles, or row blocks of 2-4 waves) gain
 // 2-2.4% from two partitions when the grid is fine (at least 16384 workgroups, 64 per CU);
 // coarser grids keep one so that every CU stays busy.  Beyond that, several partitions per
-// workgroup only cap the grid at kMaxWgs.  Paged decode keeps one (a workgroup's pages
-// must fit the block-table entries it holds).
+// workgroup only cap the grid at kMaxWgs.  16-bit paged decode keeps one; FP8 pools follow the
+// dense FP8 rule (run_splitk lowers it again if a workgroup's pages would not fit the
+// block-table entries it holds), so a paged FP8 call decomposes as the dense one does.
 int splitk_parts_per_wg(int64_t items, int n_split, bool fp8, int nw, bool paged) {
   constexpr int64_t kMaxWgs = int64_t{1} << 20, kFineGrid = int64_t{1} << 14;
   int64_t want = (items * n_split + kMaxWgs - 1) / kMaxWgs;
@@ -765,7 +809,7 @@ static hipError_t launch_split_nw(const TileArgs& a, int nw, hipStream_t stream)
 
 template <int D, class E>
 static hipError_t launch_split(const TileArgs& a, bool fp8, bool paged, int nw, hipStream_t stream) {
-  if (paged) return launch_split_nw<D, E, E, true>(a, nw, stream);
+  if (paged) return fp8 ? launch_split_nw<D, E, FP8, true>(a, nw, stream) : launch_split_nw<D, E, E, true>(a, nw, stream);
   return fp8 ? launch_split_nw<D, E, FP8, false>(a, nw, stream) : launch_split_nw<D, E, E, false>(a, nw, stream);
 }
 
@@ -823,17 +867,20 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
   a.n_split = S;
   a.split_len = split_len;
   const int64_t items = (int64_t)p.batch * p.heads_kv * a.n_rowblk;
-  a.ppw = splitk_parts_per_wg(items, S, p.kv_dtype == FA_DTYPE_FP8_E4M3, nw, kv != nullptr);
-  a.n_chunk = (S + a.ppw - 1) / a.ppw;
+  const bool fp8_kv = p.kv_dtype == FA_DTYPE_FP8_E4M3;
+  a.ppw = splitk_parts_per_wg(items, S, fp8_kv, nw, kv != nullptr && !fp8_kv);
   if (kv != nullptr) {
     // a workgroup's keys span at most (ppw * split_len - 1) / page_size + 2 pages, and it
     // holds 256 block-table entries
-    const int64_t slots = ((int64_t)a.ppw * split_len - 1) / kv->page_size + 2;
+    auto slots_for = [&](int ppw) { return ((int64_t)ppw * split_len - 1) / kv->page_size + 2; };
+    while (a.ppw > 1 && slots_for(a.ppw) > 256) --a.ppw;
+    const int64_t slots = slots_for(a.ppw);
     if (slots > 256) {
       *err = "split_len too long for the page size: a partition may span at most 256 pages";
       return FA_ERR_UNSUPPORTED;
     }
   }
+  a.n_chunk = (S + a.ppw - 1) / a.ppw;
   const int64_t total = items * a.n_chunk;
   const int64_t out_rows = (int64_t)p.batch * p.heads_q * p.seqlen_q;
   if (total > INT32_MAX || out_rows > INT32_MAX) {

@@ -7,7 +7,7 @@ are kept as aliases of the HIP-backed functions.
 """
 from .fp8 import attention_fp8, attention_fp8_triton, dequantize_kv_fp8, quantize_kv_fp8
 from .ops import attention, attention_varlen, available_backends, pack_varlen
-from .paged import attention_paged, attention_paged_reference, paged_from_dense
+from .paged import attention_paged, attention_paged_reference, paged_from_dense, paged_from_dense_fp8
 from .reference import attention_reference, attention_varlen_reference
 from .splitk import attention_splitk, attention_splitk_triton, choose_num_splits
 
@@ -25,5 +25,9 @@ __all__ = [
     "quantize_kv_fp8",
     "dequantize_kv_fp8",
     "choose_num_splits",
+    "attention_paged",
+    "attention_paged_reference",
+    "paged_from_dense",
+    "paged_from_dense_fp8",
 ]
 __version__ = "0.3.0"

@@ -22,7 +22,7 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libfused_attn_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # fa_dtype codes
 F16, BF16, F32, FP8_E4M3 = 0, 1, 2, 3
@@ -502,15 +502,38 @@ def splitk_noalloc(q, k, v, causal: bool = False, scale: Optional[float] = None,
     return (o, lse) if return_lse else o
 
 
+def _check_paged_fp8_scales(k_cache: torch.Tensor, k_scale, v_scale) -> None:
+    """FP8 pools carry 64-key block scales per page, [num_pages, Hkv, page_size / 64] floats on
+    the pools' device: the kernel indexes them by (page, kv-head, block inside the page)."""
+    if k_scale is None or v_scale is None:
+        raise RuntimeError("FP8 pools need k_scale and v_scale")
+    if k_cache.shape[2] % FP8_QBLOCK:
+        raise RuntimeError(f"FP8 pools need page_size a multiple of {FP8_QBLOCK}, got {k_cache.shape[2]}")
+    want = (k_cache.shape[0], k_cache.shape[1], k_cache.shape[2] // FP8_QBLOCK)
+    for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if tuple(t.shape) != want:
+            raise RuntimeError(f"{name} must have shape {want} (per page, kv-head and 64-key block), "
+                               f"got {tuple(t.shape)}")
+        if not t.is_floating_point() or t.dtype == _FP8:
+            raise RuntimeError(f"{name} must be a float tensor, got {t.dtype}")
+        if t.device != k_cache.device:
+            raise RuntimeError(f"{name} must be on {k_cache.device}, got {t.device}")
+
+
 def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int, causal: bool = False,
                  scale: Optional[float] = None, split_len: int = 128, workspace: Optional[torch.Tensor] = None,
-                 return_lse: bool = False):
+                 return_lse: bool = False, k_scale: Optional[torch.Tensor] = None,
+                 v_scale: Optional[torch.Tensor] = None):
     """Split-K decode over a paged cache.  q [B,Hq,Nq,D]; k_cache/v_cache [num_pages, Hkv, page_size, D]
     (any strides with unit D stride); block_table int32 [B, cols]; seqlens_k int32 [B], both on the GPU.
+    FP8 pools (float8_e4m3fn) take their block scales k_scale/v_scale [num_pages, Hkv, page_size / 64].
     With ``return_lse`` also returns the natural-log LSE, fp32 [B, Hq, Nq]."""
     if k_cache.shape != v_cache.shape or k_cache.dim() != 4:
         raise RuntimeError("k_cache and v_cache must both be [num_pages, Hkv, page_size, D]")
-    _check_qkv(q, k_cache, v_cache, "paged")
+    fp8 = k_cache.dtype == _FP8
+    _check_qkv(q, k_cache, v_cache, "paged", kv_fp8=fp8)
+    if fp8:
+        _check_paged_fp8_scales(k_cache, k_scale, v_scale)
     _require_gpu(q, k_cache, v_cache, block_table, seqlens_k)
     if block_table.dtype != torch.int32 or seqlens_k.dtype != torch.int32:
         raise RuntimeError("block_table and seqlens_k must be int32")
@@ -519,7 +542,9 @@ def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int,
         raise RuntimeError("block_table must be [B, pages] and seqlens_k [B] for q's batch B")
     lib = load_library()
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
-    q, k_cache, v_cache = _prep_qkv(q, k_cache, v_cache)
+    q, k_cache, v_cache = _prep_qkv(q, k_cache, v_cache, kv_fp8=fp8)
+    if fp8:
+        k_scale, v_scale = _prep_fp8_scales(k_cache, k_scale, v_scale)
     bt = block_table if block_table.stride(-1) == 1 else block_table.contiguous()
     sl = seqlens_k.contiguous()
     o = _new_output(q)
@@ -530,7 +555,8 @@ def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int,
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=q.device)
     lse = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if return_lse else None
-    p = make_params(q, k_cache, v_cache, o, causal, scale, lse=lse)
+    p = make_params(q, k_cache, v_cache, o, causal, scale, lse=lse, k_scale=k_scale if fp8 else None,
+                    v_scale=v_scale if fp8 else None)
     p.seqlen_k = max_k
     p.k_stride_b = p.v_stride_b = 0
     kv = PagedKV()

@@ -13,6 +13,12 @@ applied to each sequence's keys, gathered through a block table:
 
     o = attention_paged(q, k_cache, v_cache, block_table, seqlens_k)   # q, o [B, Hq, n_q, D]
 
+FP8 pools (float8_e4m3fn) hold the bytes ``quantize_kv_fp8`` writes for a
+[num_pages, Hkv, page_size, D] pool and take its block scales, fp32
+[num_pages, Hkv, page_size / 64], as ``k_scale`` / ``v_scale`` (page_size a multiple of 64):
+the semantics of ``attention_fp8_triton`` (fused_attn/fp8.py:125-147) on each sequence's
+gathered keys.
+
 ``causal`` aligns each sequence's queries to the end of its own keys (bottom-right, as
 the dense op).  On the GPU this runs the split-K HIP kernel in its paged mode; page_size
 must be a multiple of 32.  CPU tensors, or ``FUSED_ATTN_BACKEND=reference``, gather the
@@ -26,6 +32,7 @@ from typing import Optional
 import torch
 
 from . import _hip
+from .fp8 import FP8_DTYPE, QBLOCK, dequantize_kv_fp8
 from .ops import _pick_backend, default_split_len
 from .reference import attention_reference, lse_reference
 
@@ -55,12 +62,21 @@ def attention_paged_reference(q, k_cache, v_cache, block_table, seqlens_k, causa
 
 def attention_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
                     seqlens_k: torch.Tensor, causal: bool = False, scale: Optional[float] = None,
-                    max_seqlen_k: Optional[int] = None, split_len: Optional[int] = None, return_lse: bool = False):
+                    max_seqlen_k: Optional[int] = None, split_len: Optional[int] = None, return_lse: bool = False,
+                    k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None):
     """Decode attention over a paged K/V cache.  ``max_seqlen_k`` (the largest entry of
     ``seqlens_k``) sizes the grid; when omitted it is read from ``seqlens_k`` (a device sync).
+    FP8 pools take their per-page block scales ``k_scale`` / ``v_scale``.
     With ``return_lse`` also returns the natural-log LSE, fp32 [B, H_q, N_q]."""
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    fp8 = FP8_DTYPE is not None and k_cache.dtype == FP8_DTYPE
     if not q.is_cuda or _pick_backend(q) != "hip":
+        if fp8:
+            if k_scale is None or v_scale is None:
+                raise RuntimeError("FP8 pools need k_scale and v_scale")
+            if k_cache.shape[2] % QBLOCK:
+                raise RuntimeError(f"FP8 pools need page_size a multiple of {QBLOCK}")
+            k_cache, v_cache = dequantize_kv_fp8(k_cache, k_scale), dequantize_kv_fp8(v_cache, v_scale)
         return attention_paged_reference(q, k_cache, v_cache, block_table, seqlens_k, causal=causal, scale=scale,
                                          return_lse=return_lse)
     if max_seqlen_k is None:
@@ -73,7 +89,8 @@ def attention_paged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         page_size = k_cache.shape[2]
         split_len = min(split_len, max(64, (254 * page_size) // 64 * 64))
     return _hip.paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k, causal=causal, scale=scale,
-                             split_len=split_len, return_lse=return_lse)
+                             split_len=split_len, return_lse=return_lse, k_scale=k_scale if fp8 else None,
+                             v_scale=v_scale if fp8 else None)
 
 
 def paged_from_dense(k: torch.Tensor, v: torch.Tensor, page_size: int, seqlens: Optional[list] = None,
@@ -98,3 +115,45 @@ def paged_from_dense(k: torch.Tensor, v: torch.Tensor, page_size: int, seqlens: 
     block_table = perm.to(torch.int32).to(k.device)
     seqlens_k = torch.tensor(seqlens, dtype=torch.int32, device=k.device)
     return k_cache, v_cache, block_table, seqlens_k
+
+
+def paged_from_dense_fp8(k8: torch.Tensor, k_scale: torch.Tensor, v8: torch.Tensor, v_scale: torch.Tensor,
+                         page_size: int, seqlens: Optional[list] = None, extra_pages: int = 0,
+                         generator: Optional[torch.Generator] = None):
+    """Scatter a dense FP8 cache (``quantize_kv_fp8`` output: e4m3fn [B, Hkv, N, D] and fp32 block
+    scales [B, Hkv, ceil(N/64)]) into pools of ``page_size``-key pages (a multiple of 64) in a random
+    page order, with each page's block scales alongside.
+
+    Returns (k_cache, v_cache, k_scale_pool, v_scale_pool, block_table, seqlens_k): pools
+    [num_pages, Hkv, page_size, D] e4m3fn, scale pools fp32 [num_pages, Hkv, page_size / 64], an int32
+    [B, ceil(N/page_size)] block table and int32 [B] lengths.  Because pages start on 64-key blocks,
+    page p's scales are exactly the dense scales of the blocks it holds, so the pools describe the same
+    keys bit for bit.  ``extra_pages`` unused (zero) pages are added."""
+    if page_size % QBLOCK:
+        raise ValueError(f"page_size must be a multiple of {QBLOCK}")
+    b, hkv, n, d = k8.shape
+    cols = -(-n // page_size)
+    bpp = page_size // QBLOCK
+    seqlens = [n] * b if seqlens is None else list(seqlens)
+    num_pages = b * cols + extra_pages
+    perm = torch.randperm(num_pages, generator=generator, device="cpu")[:b * cols].view(b, cols)
+    idx = perm.reshape(-1).to(k8.device)
+
+    def pages(x8):
+        xb = x8.view(torch.uint8)
+        pad = cols * page_size - n
+        xb = torch.nn.functional.pad(xb, (0, 0, 0, pad)) if pad else xb
+        pool = torch.zeros(num_pages, hkv, page_size, d, dtype=torch.uint8, device=x8.device)
+        pool[idx] = xb.reshape(b, hkv, cols, page_size, d).permute(0, 2, 1, 3, 4).reshape(b * cols, hkv, page_size, d)
+        return pool.view(x8.dtype)
+
+    def scale_pages(sc):
+        pad = cols * bpp - sc.shape[-1]
+        sc = torch.nn.functional.pad(sc.float(), (0, pad)) if pad else sc.float()
+        pool = torch.zeros(num_pages, hkv, bpp, dtype=torch.float32, device=sc.device)
+        pool[idx] = sc.reshape(b, hkv, cols, bpp).permute(0, 2, 1, 3).reshape(b * cols, hkv, bpp)
+        return pool
+
+    block_table = perm.to(torch.int32).to(k8.device)
+    seqlens_k = torch.tensor(seqlens, dtype=torch.int32, device=k8.device)
+    return pages(k8), pages(v8), scale_pages(k_scale), scale_pages(v_scale), block_table, seqlens_k

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 4
+#define FA_ABI_VERSION 5
 
 /* Element types (reference: DType, csrc/flash_attn.h:7). */
 typedef enum fa_dtype {
@@ -153,9 +153,16 @@ typedef struct fa_paged_kv {
    combine, workspace size and split_len rules) with each sequence's keys gathered
    through its block table and its own length seqlens_k[b]; p->seqlen_k is the largest
    length (it sizes the grid) and the causal mask is bottom-right per sequence.
-   f16/bf16, D in {64, 128, 256}.  The reference lists paged K/V for its decode kernels as a
+   f16/bf16 q, D in {64, 128, 256}.  The reference lists paged K/V for its decode kernels as a
    roadmap item (README.md:224); the semantics are those of attention_splitk_triton
-   (fused_attn/triton_splitk.py:140-181) applied to each sequence's gathered keys. */
+   (fused_attn/triton_splitk.py:140-181) applied to each sequence's gathered keys.
+   FP8 pools (p->kv_dtype == FA_DTYPE_FP8_E4M3): the semantics of attention_fp8_triton
+   (fused_attn/fp8.py:125-147) on each sequence's gathered keys.  page_size must then be a
+   multiple of 64 and p->k_scale / p->v_scale point at fp32 scale pools
+   [num_pages, Hkv, page_size / 64] (the 64-key block scales of each page, as
+   fused_attn/fp8.py:31-45 computes them for a [num_pages, Hkv, page_size, D] pool), with
+   p->scale_stride_b the elements between pages and p->scale_stride_h between heads; the
+   blocks of a page are contiguous.  A page outside [0, num_pages) reads as zero keys. */
 fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* kv, int32_t split_len,
                                     void* workspace, size_t workspace_bytes, void* stream);
 

@@ -335,6 +335,16 @@ def attention_paged(q, k_cache, v_cache, block_table, seqlens_k, causal: bool = 
     return out
 
 
+def attention_paged_fp8(q, k8_pool, k_scale_pool, v8_pool, v_scale_pool, block_table, seqlens_k,
+                        causal: bool = False, scale: Optional[float] = None):
+    """FP8 paged pools: each page dequantised with its own 64-key block scales (a pool is a
+    [num_pages, H, page_size, D] cache to fp8.py:48-56), then the paged oracle.  The reference
+    judges FP8 attention against the fp32 oracle on the dequantised K/V
+    (tests/test_splitk_fp8.py:85); its roadmap's paged K/V (README.md:224) has no code."""
+    return attention_paged(q, dequantize_kv_fp8(k8_pool, k_scale_pool), dequantize_kv_fp8(v8_pool, v_scale_pool),
+                           block_table, seqlens_k, causal=causal, scale=scale)
+
+
 # ---------------------------------------------------------------------------------------------
 # split-K (fused_attn/triton_splitk.py)
 # ---------------------------------------------------------------------------------------------

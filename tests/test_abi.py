@@ -42,7 +42,7 @@ def test_struct_layout_matches_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _hip.ABI_VERSION == 4
+    assert lib.fa_abi_version() == _hip.ABI_VERSION == 5
 
 
 def test_choose_num_splits_known_answers(lib):
@@ -306,8 +306,12 @@ def test_paged_struct_layout(lib):
     (dict(k_page_stride=2 * 64 * 64 + 4), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "page strides"),
     (dict(v_page_stride=-8), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "page strides"),
     ({}, {}, 100, _hip.FA_ERR_INVALID_ARGUMENT, "split_len"),
-    ({}, dict(kv_dtype=_hip.FP8_E4M3, k_scale=0x50000, v_scale=0x50000), 128, _hip.FA_ERR_INVALID_ARGUMENT,
-     "k/v dtype"),
+    # FP8 pools: 64-key scale blocks must not straddle pages; scales are required and their strides checked
+    (dict(page_size=32), dict(kv_dtype=_hip.FP8_E4M3, k_scale=0x50000, v_scale=0x50000), 128,
+     _hip.FA_ERR_INVALID_ARGUMENT, "multiple of 64"),
+    ({}, dict(kv_dtype=_hip.FP8_E4M3), 128, _hip.FA_ERR_INVALID_ARGUMENT, "k_scale"),
+    ({}, dict(kv_dtype=_hip.FP8_E4M3, k_scale=0x50000, v_scale=0x50000, scale_stride_b=-1), 128,
+     _hip.FA_ERR_INVALID_ARGUMENT, "scale stride"),
     ({}, dict(lse=0x30000, lse_stride_h=-1), 128, _hip.FA_ERR_INVALID_ARGUMENT, "LSE"),
     ({}, dict(dtype=_hip.F32, kv_dtype=_hip.F32), 128, _hip.FA_ERR_UNSUPPORTED, "dtype"),
     ({}, dict(head_dim=32, q_stride_b=4 * 16 * 32, q_stride_h=16 * 32, q_stride_n=32), 128, _hip.FA_ERR_UNSUPPORTED,

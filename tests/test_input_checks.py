@@ -101,6 +101,29 @@ def test_fp8_scales_of_any_float_dtype_become_fp32():
     assert a.data_ptr() == f.data_ptr()
 
 
+@pytest.mark.skipif(FP8 is None, reason="torch has no float8_e4m3fn")
+def test_paged_fp8_pools_and_scales_are_checked():
+    q = t(2, 8, 1, 64)
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    sl = torch.full((2,), 100, dtype=torch.int32)
+    k8 = torch.zeros(10, 2, 64, 64, dtype=FP8)
+    good = torch.ones(10, 2, 1)
+    with pytest.raises(RuntimeError, match="need k_scale"):
+        _hip.paged_decode(q, k8, k8, bt, sl, 100)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        k32 = torch.zeros(10, 2, 32, 64, dtype=FP8)
+        _hip.paged_decode(q, k32, k32, bt, sl, 100, k_scale=torch.ones(10, 2, 1), v_scale=torch.ones(10, 2, 1))
+    with pytest.raises(RuntimeError, match="k_scale must have shape"):
+        _hip.paged_decode(q, k8, k8, bt, sl, 100, k_scale=torch.ones(2, 2, 2), v_scale=good)
+    with pytest.raises(RuntimeError, match="v_scale must have shape"):
+        _hip.paged_decode(q, k8, k8, bt, sl, 100, k_scale=good, v_scale=torch.ones(10, 1, 1))
+    with pytest.raises(RuntimeError, match="float8_e4m3fn"):
+        _hip.paged_decode(q, k8, t(10, 2, 64, 64), bt, sl, 100, k_scale=good, v_scale=good)
+    # consistent FP8 pools pass every check and stop at the device test
+    with pytest.raises(RuntimeError, match="needs GPU tensors"):
+        _hip.paged_decode(q, k8, k8, bt, sl, 100, k_scale=good, v_scale=good.half())
+
+
 def test_valid_cpu_inputs_reach_the_gpu_requirement():
     # consistent shapes pass every check and stop at the device test, not earlier
     with pytest.raises(RuntimeError, match="needs GPU tensors"):

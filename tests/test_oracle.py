@@ -319,6 +319,41 @@ def test_paged_oracle_equals_dense_attention_on_the_scattered_keys(causal):
     assert torch.all(got[1] == 0)  # no keys -> zeros
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_paged_fp8_oracle_equals_dense_fp8_attention(causal):
+    """Pages of 64*m keys start on 64-key scale blocks, so scattering a dense FP8 cache's bytes and
+    block scales into shuffled pages must reproduce the dense FP8 oracle exactly, per sequence."""
+    gen = torch.Generator().manual_seed(13)
+    b, hq, hkv, n, d, ps = 3, 4, 2, 200, 16, 128
+    q = torch.randn(b, hq, 2, d, generator=gen)
+    k8, ks = orc.quantize_kv_fp8(torch.randn(b, hkv, n, d, generator=gen) * 3)
+    v8, vs = orc.quantize_kv_fp8(torch.randn(b, hkv, n, d, generator=gen) * 0.01)
+    cols, bpp = -(-n // ps), ps // 64
+    perm = torch.randperm(b * cols + 2, generator=gen)[:b * cols].view(b, cols)
+    npages = b * cols + 2
+
+    def scatter(x8, sc):
+        pool = torch.zeros(npages, hkv, ps, d, dtype=torch.uint8)
+        spool = torch.rand(npages, hkv, bpp, generator=gen) + 5.0  # unused pages: garbage scales
+        xb = torch.cat([x8.view(torch.uint8), torch.zeros(b, hkv, cols * ps - n, d, dtype=torch.uint8)], dim=2)
+        scp = torch.cat([sc, torch.zeros(b, hkv, cols * bpp - sc.shape[-1])], dim=2)
+        for bi in range(b):
+            for c in range(cols):
+                pool[perm[bi, c]] = xb[bi, :, c * ps:(c + 1) * ps]
+                spool[perm[bi, c]] = scp[bi, :, c * bpp:(c + 1) * bpp]
+        return pool.view(x8.dtype), spool
+
+    k8p, ksp = scatter(k8, ks)
+    v8p, vsp = scatter(v8, vs)
+    lens = torch.tensor([200, 0, 129], dtype=torch.int32)
+    got = orc.attention_paged_fp8(q, k8p, ksp, v8p, vsp, perm.to(torch.int32), lens, causal=causal)
+    for bi, ln in enumerate(lens.tolist()):
+        want = orc.attention(q[bi:bi + 1], orc.dequantize_kv_fp8(k8, ks)[bi:bi + 1, :, :ln],
+                             orc.dequantize_kv_fp8(v8, vs)[bi:bi + 1, :, :ln], causal=causal)
+        assert torch.equal(got[bi:bi + 1], want)
+    assert torch.all(got[1] == 0)
+
+
 def test_paged_oracle_out_of_pool_pages_read_as_zero_keys():
     gen = torch.Generator().manual_seed(12)
     k = torch.randn(1, 1, 96, 8, generator=gen)

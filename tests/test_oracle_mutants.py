@@ -55,6 +55,7 @@ LSE_BRUTE = (pins.test_lse_matches_float64_bruteforce, dict(shape=(1, 2, 2, 9, 4
 LSE_BRUTE_GQA = (pins.test_lse_matches_float64_bruteforce, dict(shape=(2, 4, 2, 13, 13, 32), causal=False))
 LSE_CLOSED = (pins.test_lse_closed_forms, {})
 PAGED_OOB = (pins.test_paged_oracle_out_of_pool_pages_read_as_zero_keys, {})
+PAGED_FP8 = (pins.test_paged_fp8_oracle_equals_dense_fp8_attention, dict(causal=False))
 
 MUTANTS = {
     # causal mask and its bottom-right alignment (reference.py:24-33)
@@ -116,6 +117,9 @@ MUTANTS = {
     "page_row_from_page_number": ("paged_gather", "cache[pg, :, n % page_size]", "cache[pg, :, n // page_size]",
                                   [PAGED]),
     "negative_page_wraps": ("paged_gather", "if 0 <= pg < num_pages:", "if pg < num_pages:", [PAGED_OOB]),
+    # FP8 pools: each pool dequantised with its own scales
+    "paged_fp8_scales_swapped": ("attention_paged_fp8", "dequantize_kv_fp8(k8_pool, k_scale_pool)",
+                                 "dequantize_kv_fp8(k8_pool, v_scale_pool)", [PAGED_FP8]),
 }
 
 
