@@ -301,7 +301,7 @@ attn_fwd_kernel(const TileArgs a) {
     // max step v: scores 2v and 2v+1 of S_{t+1}
     auto max_step = [&](int v) __attribute__((always_inline)) {
       const int kb = v / 8, r = 2 * (v % 8);
-      mx = vmax(mx, vmax(nxt[kb][r], nxt[kb][r + 1]));
+      mx = vmax(vmax(mx, nxt[kb][r]), nxt[kb][r + 1]);  // one v_maximum3 per two scores
     };
 
 #pragma unroll
