@@ -504,6 +504,8 @@ def run_only(which, steps, warmup):
     if which == "prefill":
         flops, wall, ev, _, _ = bench_prefill(steps, warmup, with_sdpa=False)
         print(f"prefill: {flops / ev / 1e12:.1f} TFLOP/s kernel, {ev * 1e3:.4f} ms", flush=True)
+    elif which == "prefill_other":
+        print(json.dumps(bench_prefill_extras(steps, warmup)), flush=True)
     elif which == "quantize":
         print(json.dumps(bench_quantize(steps, warmup)), flush=True)
     elif which in ("decode", "decode128"):
@@ -520,7 +522,8 @@ def main():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
-    p.add_argument("--only", choices=["prefill", "decode", "decode128", "quantize", "copy"], default=None,
+    p.add_argument("--only", choices=["prefill", "prefill_other", "decode", "decode128", "quantize", "copy"],
+                   default=None,
                    help="run one workload without the JSON line (for profiler runs)")
     a = p.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -5,6 +5,9 @@
 //   v_mfma_f32_32x32x16_{bf16,f16}:  A[i][k]: lane l holds i = l%32, k = 8*(l/32) + 0..7
 //                                    B[k][j]: lane l holds j = l%32, k = 8*(l/32) + 0..7
 //                                    C[i][j]: lane l, acc r holds i = 8*(r/4) + 4*(l/32) + r%4, j = l%32
+//   v_mfma_f32_16x16x32_{bf16,f16}:  A[i][k]: lane l holds i = l%16, k-group l/16 (8 values)
+//                                    B[k][j]: lane l holds j = l%16, k-group l/16 (8 values)
+//                                    C[i][j]: lane l, acc r holds i = 4*(l/16) + r, j = l%16
 //   ds_read_b64_tr_b16: in each 16-lane group, lane i receives element (i%4) of the
 //                       8-byte rows addressed by lanes (i/4) + 4e, e = 0..3.
 //   v_permlane32_swap(x, x): {r0, r1} with max(r0, r1) = max(x[l], x[l^32]).
@@ -15,6 +18,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 namespace fa {
 
@@ -56,6 +61,34 @@ template <>
 __device__ __forceinline__ f32x16 mfma32<F16>(const u32x4& a, const u32x4& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
                                                 0, 0);
+}
+
+template <class E>
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c);
+template <>
+__device__ __forceinline__ f32x4 mfma16<BF16>(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16<F16>(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
+// A operand of a 16x16x32 MFMA that turns a 32x32x16 B fragment into row sums.
+// A 32x32x16 B fragment (K = 16 keys, N = 32 rows) puts row l % 32, keys 8 * (l / 32) + i in
+// lane l.  Read as the B operand of a 16x16x32 MFMA, lane l is column l % 16 and k-group
+// l / 16, so column n gathers row n (groups 0 and 2) and row n + 16 (groups 1 and 3).  With
+// A[m][k] = 1 exactly when the k-group's parity equals that of m / 4, output rows m with even
+// m / 4 sum row n and the others row n + 16; in the 16x16 output layout (lane l holds rows
+// 4 * (l / 16) .. + 3 of column l % 16) every lane then holds the full 16-key sum of its own
+// row l % 32, in all four registers.
+template <class E>
+__device__ __forceinline__ u32x4 rowsum_ones(int lane) {
+  const uint32_t one2 = std::is_same<E, BF16>::value ? 0x3f803f80u : 0x3c003c00u;
+  const uint32_t w = (((lane >> 4) ^ (lane >> 2)) & 1) ? 0u : one2;
+  return u32x4{w, w, w, w};
 }
 
 // Round-to-nearest-even pack of two fp32 into one dword of 16-bit values (lo first).
