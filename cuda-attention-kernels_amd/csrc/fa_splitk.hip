@@ -65,6 +65,18 @@ __device__ __forceinline__ void vm_wait() {
 }
 // s_waitcnt lgkmcnt(0), other counters unconstrained.
 __device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// Workgroup barrier without a memory fence (__syncthreads adds one, which waits for every
+// outstanding load, LDS DMA included).  LDS written by DMA is published by each wave's own
+// vmcnt wait before the barrier; LDS reads are retired by lgkm_wait0 before it.  One-wave
+// workgroups need no barrier, only the compiler ordering.
+template <int NW>
+__device__ __forceinline__ void wg_barrier() {
+  if constexpr (NW > 1) {
+    __asm__ volatile("s_barrier" ::: "memory");
+  } else {
+    __asm__ volatile("" ::: "memory");
+  }
+}
 
 template <int D, class E, class KV, int NW, int BN, bool PAGED, bool ONE_STAGE>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
@@ -260,6 +272,8 @@ attn_splitk_kernel(const TileArgs a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[s] = (ld16(qp + 16 * s) ^ qsign) & keep;
   }
+  // keep the Q loads ahead of the first K/V tiles' DMA: waiting for Q then leaves the tiles in flight
+  __builtin_amdgcn_sched_barrier(0);
 
   // page of key n (paged; n in [klo, khi), so its slot is among the loaded entries)
   auto page_of = [&](int n) __attribute__((always_inline)) {
@@ -560,7 +574,48 @@ attn_splitk_kernel(const TileArgs a) {
     __builtin_amdgcn_s_setprio(0);
   };
 
-  if constexpr (STAGES == 2) {
+  if constexpr (STAGES == 2 && NW > 1) {
+    // Multi-wave workgroups (speculative decode rows): two tiles in flight.  Tile t+2 is
+    // issued into tile t's stage as soon as every wave has read it.  Every step issues its
+    // refill, past the last tile with a zero-length descriptor (no memory access; the DMA
+    // writes zeros into a stage nothing reads), so each wait is the same count: loads land
+    // in issue order, and vmcnt <= 2*QPW after tile t+2's 2*QPW instructions means tile t+1
+    // landed.  The barriers carry no memory fence (__syncthreads' fence would wait for
+    // vmcnt(0)).  Measured on the 32k-key cache at n_q=16: +1.2% at 128-key partitions, +3.4%
+    // at 4096; one-wave workgroups (n_q=1) lost 1.3% with it and keep one tile in flight.
+    load_tile(klo, lds_st0);
+    load_tile(klo + BN, lds_st1);
+    vm_wait<2 * QPW>();
+    wg_barrier<NW>();
+
+    // One tile: S^T, softmax, O += P V on this stage, then refill it with tile t+2.  The
+    // stage is a compile-time choice (the loop below is unrolled by 2).
+    auto tile_step = [&](auto stage_tag, int t) __attribute__((always_inline)) {
+      constexpr int ST = decltype(stage_tag)::value;
+      uint8_t* cur = ST == 0 ? lds_st0 : lds_st1;
+      const int n0 = klo + t * BN;
+      if (wave_active && n0 < wave_khi) {
+        Ks = cur;
+        Vs = cur + TILE_BYTES;
+        f32x16 sacc[KB];
+        tile_qk(sacc);
+        tile_softmax_pv(sacc, n0);
+      }
+      lgkm_wait0();  // this wave's reads of the stage have returned
+      wg_barrier<NW>();
+      load_tile(n0 + 2 * BN, cur);
+      vm_wait<2 * QPW>();  // tile t+1 landed; tile t+2 stays in flight
+      wg_barrier<NW>();
+      // The last tile of a partition closes it.  Its stores are issued after this
+      // tile's wait, so they complete under the next tile instead of stalling this one.
+      if ((t + 1) % tiles_per_part == 0 || t + 1 == n_tiles) emit_partial(part0 + t / tiles_per_part);
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+      tile_step(std::integral_constant<int, 0>{}, t);
+      if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
+    }
+    lds_dma_wait();  // the zero-length refills past the end land before the workgroup ends
+  } else if constexpr (STAGES == 2) {
     if (n_tiles > 0) load_tile(klo, lds_st0);
     lds_dma_wait();
     __syncthreads();

@@ -23,6 +23,17 @@ def close(out: torch.Tensor, ref: torch.Tensor, tol: float) -> bool:
     return bool(((out.float() - r).abs() <= tol + tol * r.abs()).all().item())
 
 
+def check_bars(out: torch.Tensor, ref: torch.Tensor, tol: float) -> float:
+    """Assert both bars, the reference's (close) and the plain max-abs one (max_err <= tol), and print the
+    max-abs error beside the output's magnitude.  Returns the max-abs error."""
+    err = max_err(out, ref)
+    mag = ref.float().abs().max().item() if ref.numel() else 0.0
+    print(f"max_abs_err={err:.3e} |ref|max={mag:.3e} bar={tol:g}", flush=True)
+    assert close(out, ref, tol), err
+    assert err <= tol, (err, mag)
+    return err
+
+
 def announce(msg: str) -> None:
     """Name the case before GPU work starts, flushed, so a crash still identifies it."""
     print(f"[case] {msg}", flush=True)

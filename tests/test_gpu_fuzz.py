@@ -5,7 +5,8 @@ tests/test_correctness.py, test_varlen.py and test_splitk_fp8.py) with shapes no
 picked by hand: ragged lengths, every GQA ratio that divides the heads, both layouts,
 custom and negative scales.  Each case is drawn from its own seed and named before
 it runs.  The bar is the reference's assert_close(atol=tol, rtol=tol), since large
-random scales produce outputs of magnitude ~4 (see helpers.close)."""
+random scales produce outputs of magnitude ~4 (see helpers.close), and every case must also
+meet the plain max-abs bar and prints its max-abs error (helpers.check_bars)."""
 import math
 import random
 
@@ -14,7 +15,7 @@ import torch
 
 import fused_attn
 from fused_attn.triton_fwd import attention_triton
-from helpers import FP8_TOL, TOL, announce, close, max_err, randn
+from helpers import FP8_TOL, TOL, announce, check_bars, randn
 from oracle import attention_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -56,7 +57,7 @@ def test_fuzz_dense(seed):
     out = fused_attn.attention(q, k, v, causal=causal, scale=scale)
     ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal, scale=scale)
     assert out.shape == q.shape and out.dtype == dtype
-    assert close(out, ref, _tol(dtype)), max_err(out, ref)
+    check_bars(out, ref, _tol(dtype))
 
 
 @pytest.mark.parametrize("seed", range(32))
@@ -79,7 +80,7 @@ def test_fuzz_splitk(seed):
     v = randn(b, hkv, n_k, d, dtype=dtype)
     out = fused_attn.attention_splitk(q, k, v, causal=causal, split_len=split_len)
     ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal)
-    assert close(out, ref, TOL[dtype]), max_err(out, ref)
+    check_bars(out, ref, TOL[dtype])
 
 
 @pytest.mark.parametrize("seed", range(16))
@@ -99,7 +100,7 @@ def test_fuzz_fp8_splitk(seed):
     v8, vs = fused_attn.quantize_kv_fp8(randn(b, hkv, n_k, d))
     out = fused_attn.attention_fp8(q, k8, ks, v8, vs, split_len=split_len)
     ref = orc.attention_fp8(q.cpu(), k8.cpu(), ks.cpu(), v8.cpu(), vs.cpu())
-    assert close(out, ref, FP8_TOL), max_err(out, ref)
+    check_bars(out, ref, FP8_TOL)
 
 
 @pytest.mark.parametrize("seed", range(24))
@@ -125,7 +126,7 @@ def test_fuzz_varlen(seed):
     out = fused_attn.attention_varlen(q, k, v, cu_q, cu_k, max_q, max_k, causal=causal)
     ref = orc.attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=causal)
     assert out.shape == q.shape
-    assert close(out, ref, _tol(dtype)), max_err(out, ref)
+    check_bars(out, ref, _tol(dtype))
 
 
 @pytest.mark.parametrize("seed", range(16))
@@ -152,7 +153,7 @@ def test_fuzz_paged(seed):
                                                  generator=torch.Generator().manual_seed(seed))
     out = fused_attn.attention_paged(q, kc, vc, bt, sl, causal=causal, split_len=split_len)
     ref = orc.attention_paged(q, kc, vc, bt, sl, causal=causal)
-    assert close(out, ref, TOL[dtype]), max_err(out, ref)
+    check_bars(out, ref, TOL[dtype])
 
 
 def test_fuzz_lse_matches_logsumexp():

@@ -5,7 +5,7 @@ import torch
 
 import fused_attn
 from fused_attn import _hip, ops
-from helpers import FP8_TOL, TOL, announce, close, max_err, randn
+from helpers import FP8_TOL, TOL, announce, check_bars, max_err, randn
 from oracle import attention_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -34,9 +34,9 @@ def test_splitk_matches_oracle(b, h_q, h_kv, n_q, n_k, d, num_splits, causal, dt
 @pytest.mark.parametrize("split_len", [64, 512])
 def test_peaked_softmax_meets_the_reference_bar(scale, split_len):
     """Large |scale| makes each row follow a few V rows of magnitude ~4, where one bf16 ulp is 0.031:
-    split-K (one more 16-bit rounding, of the normalised partials) and the prefill kernel stay within the
-    reference's assert_close(atol=2e-2, rtol=2e-2).  Found by a random sweep (B=2 Hq=64 Hkv=8 nq=982
-    nk=790)."""
+    split-K (fp32 partials) and the prefill kernel stay within the reference's
+    assert_close(atol=2e-2, rtol=2e-2) and within the plain max-abs bar of 2e-2.  Found by a random sweep
+    (B=2 Hq=64 Hkv=8 nq=982 nk=790)."""
     announce(f"peaked softmax scale={scale} split={split_len}")
     gen = torch.Generator(device="cuda").manual_seed(1478)
     q = randn(2, 64, 982, 128, dtype=torch.bfloat16, gen=gen)
@@ -44,8 +44,8 @@ def test_peaked_softmax_meets_the_reference_bar(scale, split_len):
     v = randn(2, 8, 790, 128, dtype=torch.bfloat16, gen=gen)
     ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), scale=scale)
     out = fused_attn.attention_splitk(q, k, v, scale=scale, split_len=split_len)
-    assert close(out, ref, TOL[torch.bfloat16]), max_err(out, ref)
-    assert close(fused_attn.attention(q, k, v, scale=scale), ref, TOL[torch.bfloat16])
+    check_bars(out, ref, TOL[torch.bfloat16])
+    check_bars(fused_attn.attention(q, k, v, scale=scale), ref, TOL[torch.bfloat16])
 
 
 @pytest.mark.parametrize("split_len", [64, 128, 192, 1024, 4096])
