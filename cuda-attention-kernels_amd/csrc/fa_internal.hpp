@@ -16,8 +16,8 @@ struct TileArgs {
   const void* q;
   const void* k;
   const void* v;
-  void* o;     // prefill: output in the q dtype; split-K: fp32 partials [rows, S, D]
-  float* ml;   // split-K: (max, sum) pairs [rows, S, 2]
+  void* o;     // prefill: output in the q dtype; split-K: fp32 partials (layout: part_major)
+  float* ml;   // split-K: (max, sum) pairs, laid out like the partials
   float* lse;  // prefill: optional natural-log LSE
   const float* k_scale;
   const float* v_scale;
@@ -42,6 +42,9 @@ struct TileArgs {
   int64_t sbt;       // block_table row stride
   int64_t spk, spv;  // page strides of the K and V pools
   int32_t page_size, num_pages;
+  // split-K partial layout: 0 = [B, Hq, Nq, S, D] (row-major), 1 = [B, Hkv, S, G*Nq, D]
+  // (partition-major: the rows one workgroup writes for one partition are one block)
+  int32_t part_major;
 };
 
 struct QuantArgs {
@@ -60,6 +63,8 @@ struct CombineArgs {
   float* lse;  // optional natural-log LSE [B, Hq, Nq]
   int64_t slb, slh;
   int32_t hq, nq, n_split;
+  int32_t group;       // q-heads per kv-head
+  int32_t part_major;  // partial layout, as TileArgs::part_major
 };
 
 // Number of rows (q-heads x queries) one split-K workgroup covers, and the

@@ -105,9 +105,12 @@ fa_status fa_attention_fwd(const fa_fwd_params* p, void* stream);
 fa_status fa_attention_varlen_fwd(const fa_fwd_params* p, void* stream);
 
 /* Bytes of workspace fa_attention_splitk needs for `num_splits` key partitions:
-   fp32 partial outputs [B, Hq, Nq, S, D], each normalised by its own row sum, plus fp32
-   (max, sum) pairs [B, Hq, Nq, S, 2] in the log2 domain (the reference keeps fp32
-   partials too: fused_attn/triton_splitk.py:90-96,156-158). */
+   fp32 partial outputs (B*Hq*Nq*S*D floats), each normalised by its own row sum, plus fp32
+   (max, sum) pairs (B*Hq*Nq*S*2 floats) in the log2 domain (the reference keeps fp32
+   partials too: fused_attn/triton_splitk.py:90-96,156-158).  The library lays them out as
+   [B, Hq, Nq, S, D] or, for 32 or more partitions at D <= 128, as [B, Hkv, S, G*Nq, D]
+   (G = Hq/Hkv), so that each workgroup's partials are one contiguous block; the layout is
+   internal to the split and combine kernels. */
 size_t fa_splitk_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q, int32_t head_dim,
                                  int32_t num_splits);
 
