@@ -178,7 +178,10 @@ def test_peaked_softmax_precision_splitk_vs_prefill():
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("b,h_q,h_kv,n_q,n_k,d,split_len",
                          [(2, 8, 2, 1, 3000, 128, 128), (1, 4, 1, 16, 2500, 64, 256), (2, 8, 2, 16, 8, 128, 64),
-                          (1, 4, 2, 4, 1300, 256, 512)])
+                          (1, 4, 2, 4, 1300, 256, 512),
+                          # 32 or more partitions: partition-major partials, with one-, two- and four-wave
+                          # workgroups (rows = G * n_q of 1, 64 and 128)
+                          (2, 8, 8, 1, 5000, 64, 64), (1, 8, 2, 16, 4100, 128, 128), (1, 16, 2, 16, 9000, 128, 128)])
 def test_splitk_lse_matches_oracle(b, h_q, h_kv, n_q, n_k, d, split_len, causal):
     """The combine's natural-log LSE [B, Hq, Nq] (the reference's WRITE_LSE quantity, triton_fwd.py:169-172);
     n_k < n_q causal rows see no key and report -inf."""
