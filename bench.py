@@ -302,6 +302,7 @@ def bench_decode(steps, warmup, only_128=False):
         "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
     }
     res.update(bench_paged(k, v, steps, warmup, g))
+    res.update(bench_paged(k, v, steps, warmup, g, page_size=16, splits=(128,), suffix="_16key_pages"))
     del k, v
     torch.cuda.empty_cache()
     c = FP8_DECODE
@@ -375,8 +376,8 @@ def bench_decode_d256(steps, warmup, g):
     return res
 
 
-def bench_paged(k, v, steps, warmup, g, page_size=64):
-    """Split-K decode over the same K/V scattered into a shuffled pool of 64-key pages."""
+def bench_paged(k, v, steps, warmup, g, page_size=64, splits=(128, None), suffix=""):
+    """Split-K decode over the same K/V scattered into a shuffled pool of `page_size`-key pages."""
     import torch
 
     import fused_attn
@@ -385,13 +386,14 @@ def bench_paged(k, v, steps, warmup, g, page_size=64):
     kc, vc, bt, sl = fused_attn.paged_from_dense(k, v, page_size, generator=torch.Generator().manual_seed(0))
     q = torch.randn(c["b"], c["hq"], 1, c["d"], device="cuda", generator=g).bfloat16()
     res = {}
-    for split in (128, None):
+    for split in splits:
         keys = split or fused_attn.ops.default_split_len(1, c["nk"], c["b"], c["hkv"], c["hq"] // c["hkv"])
+        keys = min(keys, max(64, (254 * page_size) // 64 * 64))  # as the op caps it for small pages
         fn = lambda: fused_attn.attention_paged(q, kc, vc, bt, sl, max_seqlen_k=c["nk"], split_len=keys)  # noqa: E731
         err = _batch0_err(fn(), q, k, v, False)  # the pool holds the dense K/V, shuffled into pages
         wall, ev = _time_calls(fn, steps, warmup)
         nbytes = 2 * kc.numel() * 2 + 2 * q.numel() * 2 + bt.numel() * 4
-        res["paged_decode" + ("" if split else "_default_split")] = {
+        res["paged_decode" + suffix + ("" if split else "_default_split")] = {
             "workload": f"paged split-K B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 n_k={c['nk']} D={c['d']} bf16, "
                         f"{page_size}-key pages in shuffled order, {keys}-key partitions + LSE combine"
                         f"{'' if split else ' (default partition policy)'}",

@@ -78,7 +78,7 @@ __device__ __forceinline__ void wg_barrier() {
   }
 }
 
-template <int D, class E, class KV, int NW, int BN, bool PAGED, bool ONE_STAGE>
+template <int D, class E, class KV, int NW, int BN, bool PAGED, bool ONE_STAGE, int PGS>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 attn_splitk_kernel(const TileArgs a) {
   using Shape = TileShape<D, BN>;    // 16-bit tiles
@@ -93,6 +93,10 @@ attn_splitk_kernel(const TileArgs a) {
   static_assert(BN % 32 == 0 && D % 32 == 0 && (D == 64 || D == 128 || D == 256), "tile shape");
   static_assert(TILE_BYTES % (1024 * NW) == 0, "tile loads must split evenly over the waves");
   constexpr int PG_REGS = 4;  // paged: block-table entries held per lane (64 * PG_REGS per workgroup)
+  // paged: keys per page group, the unit one buffer descriptor covers (32, or 16 for pages of
+  // 16 + 32k keys); a 1-KiB DMA block holds 2-8 whole rows, so it never straddles a group
+  constexpr int NPG = BN / PGS;
+  static_assert(PGS == 16 || PGS == 32, "page group");
   constexpr float NEG_INF = -__builtin_inff();
 
   // Two LDS stages (tile t+1 loads while tile t is read), or, for one-wave workgroups, a
@@ -220,7 +224,7 @@ attn_splitk_kernel(const TileArgs a) {
   // ---- paged: the block-table entries of keys [klo, khi) --------------------------
   int pg[PG_REGS] = {};
   int first_slot = 0;
-  int first_pages[KB];  // the first tile's pages: uniform loads through the scalar cache,
+  int first_pages[NPG];  // the first tile's pages: uniform loads through the scalar cache,
                         // which the K/V stream does not evict, so the first DMA waits little
   if constexpr (PAGED) {
     // bounded by the grid's largest length, not this sequence's, so that this load does
@@ -231,8 +235,8 @@ attn_splitk_kernel(const TileArgs a) {
     const int slot_end = kgrid > klo ? (kgrid - 1) / a.page_size + 1 : first_slot;
     const int32_t* bt = a.block_table + (int64_t)b * a.sbt;
 #pragma unroll
-    for (int h = 0; h < KB; ++h) {
-      const int nh = klo + 32 * h;
+    for (int h = 0; h < NPG; ++h) {
+      const int nh = klo + PGS * h;
       first_pages[h] = nh < kgrid ? bt[nh / a.page_size] : -1;
     }
 #pragma unroll
@@ -285,13 +289,13 @@ attn_splitk_kernel(const TileArgs a) {
     if (rel >= 192) v = __builtin_amdgcn_readlane(pg[3], ln);
     return v;
   };
-  // paged: descriptors of the 32-key half-tiles starting at n0 (+32); keys at or past
+  // paged: descriptors of the PGS-key groups of the tile starting at n0; keys at or past
   // khi, and pages outside the pool, are beyond the byte limit and read as zeros
   auto paged_resources = [&](int n0, __amdgpu_buffer_rsrc_t* rk, __amdgpu_buffer_rsrc_t* rv) __attribute__((always_inline)) {
 #pragma unroll
-    for (int h = 0; h < KB; ++h) {
-      const int nh = n0 + 32 * h;
-      const int valid = min(khi - nh, 32);
+    for (int h = 0; h < NPG; ++h) {
+      const int nh = n0 + PGS * h;
+      const int valid = min(khi - nh, PGS);
       const int page = valid <= 0 ? -1 : (n0 == klo ? first_pages[h] : page_of(nh));
       const bool ok = valid > 0 && (uint32_t)page < (uint32_t)a.num_pages;
       const int64_t off = ok ? (int64_t)(nh % a.page_size) : 0;
@@ -321,21 +325,28 @@ attn_splitk_kernel(const TileArgs a) {
   // Each wave fills QPW 1-KiB blocks of the K and of the V tile straight from memory.
   auto load_parts = [&](int n0, uint8_t* kl, uint8_t* vl, bool do_k, bool do_v) __attribute__((always_inline)) {
     if constexpr (PAGED) {
-      __amdgpu_buffer_rsrc_t rk[KB], rv[KB];
+      __amdgpu_buffer_rsrc_t rk[NPG], rv[NPG];
       paged_resources(n0, rk, rv);
 #pragma unroll
       for (int i = 0; i < QPW; ++i) {
         const int blk = wave * QPW + i;
         const int byte = blk * 1024 + lane * 16;
         const int r = byte / (D * KV::bytes), p = (byte % (D * KV::bytes)) / 16;
-        // a 1-KiB block holds 4 or 8 whole rows of one 32-key half (kperm keeps the half)
-        const int half = (blk * 1024 / (D * KV::bytes)) / 32;
-        const __amdgpu_buffer_rsrc_t ck = (KB > 1 && half) ? rk[KB - 1] : rk[0];
-        const __amdgpu_buffer_rsrc_t cv = (KB > 1 && half) ? rv[KB - 1] : rv[0];
+        // a 1-KiB block holds 2-8 whole rows of one page group (kperm only swaps key bits 2
+        // and 3, so it keeps a row in its 16-key group)
+        const int grp = (blk * 1024 / (D * KV::bytes)) / PGS;  // wave-uniform
+        __amdgpu_buffer_rsrc_t ck = rk[0], cv = rv[0];
+#pragma unroll
+        for (int h = 1; h < NPG; ++h) {
+          if (grp == h) {
+            ck = rk[h];
+            cv = rv[h];
+          }
+        }
         const int sk = IS_FP8 ? Shape8::swz_k(r) : Shape::swz_k(r);
         const int sv = IS_FP8 ? Shape8::swz_v(r) : Shape::swz_v(r);
-        if (do_k) lds_dma16<true>(ck, kl + blk * 1024, (kperm(r) - 32 * half) * (int)krow_bytes + ((p ^ sk) * 16));
-        if (do_v) lds_dma16<true>(cv, vl + blk * 1024, (r - 32 * half) * (int)vrow_bytes + ((p ^ sv) * 16));
+        if (do_k) lds_dma16<true>(ck, kl + blk * 1024, (kperm(r) - PGS * grp) * (int)krow_bytes + ((p ^ sk) * 16));
+        if (do_v) lds_dma16<true>(cv, vl + blk * 1024, (r - PGS * grp) * (int)vrow_bytes + ((p ^ sv) * 16));
       }
       return;
     }
@@ -820,8 +831,16 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const CombineArgs c
 
 template <int D, class E, class KV, int NW, int BN, bool PAGED, bool ONE_STAGE = false>
 static hipError_t launch_splitk(const TileArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_splitk_kernel<D, E, KV, NW, BN, PAGED, ONE_STAGE>), dim3((unsigned)a.total), dim3(NW * 64),
-                     0, stream, a);
+  // paged pools of 16 + 32k keys per page take 16-key page groups (twice the descriptors)
+  if constexpr (PAGED && KV::bytes == 2) {
+    if (a.page_size % 32 != 0) {
+      hipLaunchKernelGGL((attn_splitk_kernel<D, E, KV, NW, BN, PAGED, ONE_STAGE, 16>), dim3((unsigned)a.total),
+                         dim3(NW * 64), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((attn_splitk_kernel<D, E, KV, NW, BN, PAGED, ONE_STAGE, 32>), dim3((unsigned)a.total),
+                     dim3(NW * 64), 0, stream, a);
   return hipGetLastError();
 }
 

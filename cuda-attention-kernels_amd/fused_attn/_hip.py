@@ -22,7 +22,7 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libfused_attn_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # fa_dtype codes
 F16, BF16, F32, FP8_E4M3 = 0, 1, 2, 3

@@ -21,7 +21,7 @@ gathered keys.
 
 ``causal`` aligns each sequence's queries to the end of its own keys (bottom-right, as
 the dense op).  On the GPU this runs the split-K HIP kernel in its paged mode; page_size
-must be a multiple of 32.  CPU tensors, or ``FUSED_ATTN_BACKEND=reference``, gather the
+must be a multiple of 16 (64 for FP8 pools).  CPU tensors, or ``FUSED_ATTN_BACKEND=reference``, gather the
 pages and run the unfused reference per sequence.
 """
 from __future__ import annotations

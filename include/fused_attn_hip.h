@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 5
+#define FA_ABI_VERSION 6
 
 /* Element types (reference: DType, csrc/flash_attn.h:7). */
 typedef enum fa_dtype {
@@ -144,7 +144,7 @@ typedef struct fa_paged_kv {
   const int32_t* block_table;  /* [batch, block_table_cols] page indices, on the device */
   int64_t block_table_stride;  /* elements between rows of block_table */
   int32_t block_table_cols;    /* pages per sequence in the table; cols * page_size >= p->seqlen_k */
-  int32_t page_size;           /* keys per page: a positive multiple of 32 */
+  int32_t page_size;           /* keys per page: a positive multiple of 16 (64 for FP8 pools) */
   const int32_t* seqlens_k;    /* [batch] keys per sequence, on the device; values above p->seqlen_k
                                   are read as p->seqlen_k, negative values as 0 */
   int32_t num_pages;           /* pages per pool; a table entry outside [0, num_pages) reads as zero keys */

@@ -42,7 +42,7 @@ def test_struct_layout_matches_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _hip.ABI_VERSION == 5
+    assert lib.fa_abi_version() == _hip.ABI_VERSION == 6
 
 
 def test_choose_num_splits_known_answers(lib):
@@ -295,8 +295,8 @@ def test_paged_struct_layout(lib):
 
 
 @pytest.mark.parametrize("kv_over,p_over,split,code,msg", [
-    (dict(page_size=48), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "multiple of 32"),
-    (dict(page_size=0), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "multiple of 32"),
+    (dict(page_size=40), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "multiple of 16"),
+    (dict(page_size=0), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "multiple of 16"),
     (dict(num_pages=-1), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "negative"),
     (dict(block_table_cols=3), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "fewer pages"),
     (dict(block_table=0), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "non-NULL"),

@@ -134,7 +134,7 @@ def test_fuzz_paged(seed):
     rng = random.Random(4000 + seed)
     dtype = rng.choice([torch.bfloat16, torch.float16])
     d = rng.choice([64, 128, 256])
-    page = rng.choice([32, 64, 96, 128])
+    page = rng.choice([16, 32, 48, 64, 96, 128])
     hkv = rng.choice([1, 2, 4])
     hq = hkv * rng.choice([1, 4])
     b = rng.randint(1, 5)

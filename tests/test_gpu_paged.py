@@ -27,7 +27,7 @@ def _dense_and_paged(b, hq, hkv, nq, n, d, page, dtype, lens=None, seed=0, extra
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("d", [64, 128, 256])
-@pytest.mark.parametrize("page", [32, 64, 256])
+@pytest.mark.parametrize("page", [16, 32, 48, 64, 256])
 @pytest.mark.parametrize("nq,causal", [(1, False), (4, True), (20, True)])
 def test_paged_matches_oracle(dtype, d, page, nq, causal):
     announce(f"paged oracle {dtype} d={d} page={page} nq={nq} causal={causal}")
@@ -48,6 +48,21 @@ def test_paged_is_bit_identical_to_dense_splitk(split_len, nq, causal):
     announce(f"paged == dense split_len={split_len} nq={nq} causal={causal}")
     q, k, v, kc, vc, bt, sl = _dense_and_paged(3, 16, 4, nq, 777, 128, 64, torch.bfloat16)
     sk = split_len or fused_attn.ops.default_split_len(nq, 777, 3, 4, 4)
+    dense = fused_attn.attention_splitk(q, k, v, causal=causal, split_len=sk)
+    paged = fused_attn.attention_paged(q, kc, vc, bt, sl, causal=causal, split_len=sk)
+    assert torch.equal(dense, paged)
+
+
+@pytest.mark.parametrize("page", [16, 48])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("split_len", [64, 128, 512, None])
+@pytest.mark.parametrize("nq,causal", [(1, False), (16, True), (20, True)])
+def test_paged_small_pages_bit_identical_to_dense_splitk(page, d, split_len, nq, causal):
+    """Pages of 16 + 32k keys (vLLM's 16-key pages): the tile is fetched in 16-key page groups,
+    and the result still equals the dense split-K kernel bit for bit."""
+    announce(f"paged small pages == dense page={page} d={d} split_len={split_len} nq={nq} causal={causal}")
+    q, k, v, kc, vc, bt, sl = _dense_and_paged(2, 8, 2, nq, 700, d, page, torch.bfloat16)
+    sk = split_len or fused_attn.ops.default_split_len(nq, 700, 2, 2, 4)
     dense = fused_attn.attention_splitk(q, k, v, causal=causal, split_len=sk)
     paged = fused_attn.attention_paged(q, kc, vc, bt, sl, causal=causal, split_len=sk)
     assert torch.equal(dense, paged)
@@ -94,6 +109,20 @@ def test_paged_many_pages_per_partition():
         assert torch.equal(dense, paged), split_len
     with pytest.raises(RuntimeError, match="256 pages"):
         fused_attn.attention_paged(q, kc, vc, bt, sl, split_len=8256)
+
+
+def test_paged_16_key_pages_many_per_partition():
+    """16-key pages: a 4032-key partition spans 254 of them (within the 256 block-table entries a
+    workgroup holds), 4096 keys would need 258; without split_len the op caps the partition so
+    that it fits."""
+    announce("paged 16-key pages, long partitions")
+    q, k, v, kc, vc, bt, sl = _dense_and_paged(2, 4, 1, 1, 9000, 128, 16, torch.float16)
+    dense = fused_attn.attention_splitk(q, k, v, split_len=4032)
+    assert torch.equal(fused_attn.attention_paged(q, kc, vc, bt, sl, split_len=4032), dense)
+    with pytest.raises(RuntimeError, match="256 pages"):
+        fused_attn.attention_paged(q, kc, vc, bt, sl, split_len=4096)
+    out = fused_attn.attention_paged(q, kc, vc, bt, sl)
+    assert max_err(out, orc.attention_paged(q, kc, vc, bt, sl)) <= TOL[torch.float16]
 
 
 def test_paged_out_of_pool_entries_read_as_zero_keys():
