@@ -45,6 +45,7 @@ struct TileArgs {
   // split-K partial layout: 0 = [B, Hq, Nq, S, D] (row-major), 1 = [B, Hkv, S, G*Nq, D]
   // (partition-major: the rows one workgroup writes for one partition are one block)
   int32_t part_major;
+  int32_t o16;  // prefill: O base and strides allow 16-byte stores
 };
 
 struct QuantArgs {

@@ -135,15 +135,16 @@ attn_fwd_kernel(const TileArgs a) {
   const float c = fmaxf(fabsf(a.qk_scale), kMinScale);
 
   // ---- Q fragments (B operand of S^T), resident for the whole kernel ----------------
-  // (rows past the end read row 0, which exists, and are zeroed)
+  // (rows past the end read row 0, which exists, and are zeroed).  They are loaded in the
+  // prologue after the first K/V tiles' DMA is issued, so that both latencies overlap.
   u32x4 qf[KS];
-  {
+  auto load_q = [&]() __attribute__((always_inline)) {
     const int64_t qrow = qtok0 + (row_ok ? qi : 0);
     const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + qrow * a.sqn + 8 * g;
     const uint32_t keep = row_ok ? 0xffffffffu : 0u;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[s] = (ld16(qp + 16 * s) ^ qsign) & keep;
-  }
+  };
 
   // ---- K/V tiles: global -> LDS --------------------------------------------------------
   // Buffer loads past the byte limit return zeros, which zero-fills the keys >= khi of
@@ -377,6 +378,10 @@ attn_fwd_kernel(const TileArgs a) {
     load_k(0, k_buf0);
     load_v(0, v_buf0);
     if (n_tiles > 1) load_k(BN, k_buf1);
+    // the Q loads go out behind the DMA (the sign/row fix-up waits for them, and would
+    // otherwise hold the DMA back by a memory round trip)
+    __builtin_amdgcn_sched_barrier(0);
+    load_q();
     lds_dma_wait();
     __syncthreads();
 #pragma unroll
@@ -419,22 +424,53 @@ attn_fwd_kernel(const TileArgs a) {
   if (!wave_active) return;
   // each lane summed its 16 of the row's keys per tile (or holds the full sum, MFMA_ROWSUM)
   const float l_tot = MFMA_ROWSUM ? l_acc[0] : sum_xor32(l_run);
-  if (!row_ok) return;
   // Rows that saw no key have l == 0 and emit zeros (triton_fwd.py:163-165).
   const float l_safe = (l_tot == 0.f) ? 1.f : l_tot;
   const float inv = 1.f / l_safe;
-  uint16_t* op = (uint16_t*)a.o + (int64_t)b * a.sob + (int64_t)hq * a.soh + (qtok0 + qi) * a.son;
+  // O is staged through LDS, row-major with 16-byte chunks XOR-swizzled by row, and written
+  // back in whole rows: a lane of the O^T fragment holds 4 values of each of 16 chunks of one
+  // row, so storing from the fragment sends each instruction to 32 rows (32 partial cache
+  // lines); from LDS, 16 consecutive lanes write one row's 256 bytes (D=128).  Every wave has
+  // passed the last tile's barrier and its DMA has landed, so the K/V buffers are free; each
+  // wave takes its own 32*D-element region of them.
+  {
+    constexpr int NCH = D / 8;                       // 16-byte chunks per row
+    constexpr int SWZ = NCH < 16 ? NCH - 1 : 15;     // chunk swizzle by row
+    constexpr int REG = 32 * D;                      // elements per wave
+    constexpr int PER_BUF = TILE / REG;              // wave regions per buffer
+    static_assert(PER_BUF >= 1 && VTILE >= TILE && NW <= 4 * PER_BUF, "O staging must fit the K/V buffers");
+    const int bi = wave / PER_BUF;
+    uint16_t* stage = (bi == 0 ? k_buf0 : bi == 1 ? k_buf1 : bi == 2 ? v_buf0 : v_buf1) + (wave % PER_BUF) * REG;
 #pragma unroll
-  for (int d = 0; d < DB; ++d) {
+    for (int d = 0; d < DB; ++d) {
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      if (d * 32 + 8 * rq >= D) continue;  // D=16: O^T rows 16..31 are padding
-      const int d0 = d * 32 + 8 * rq + 4 * g;
-      st8(op + d0, u32x2{pack2<E>(oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv),
-                         pack2<E>(oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv)});
+      for (int rq = 0; rq < 4; ++rq) {
+        if (d * 32 + 8 * rq >= D) continue;  // D=16: O^T rows 16..31 are padding
+        const int c = 4 * d + rq;            // chunk of d values d*32 + 8*rq .. +7; this lane holds half g
+        *reinterpret_cast<u32x2*>(stage + j * D + ((c ^ (j & SWZ)) * 8) + 4 * g) =
+            u32x2{pack2<E>(oacc[d][4 * rq] * inv, oacc[d][4 * rq + 1] * inv),
+                  pack2<E>(oacc[d][4 * rq + 2] * inv, oacc[d][4 * rq + 3] * inv)};
+      }
+    }
+    constexpr int RPI = 64 / NCH;  // rows per 64-lane read
+    const int cc = lane % NCH;
+    uint16_t* obase = (uint16_t*)a.o + (int64_t)b * a.sob + (int64_t)hq * a.soh + (qtok0 + wr0) * a.son;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = i * RPI + lane / NCH;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * D + ((cc ^ (r & SWZ)) * 8));
+      if (wr0 + r < seq_q) {
+        uint16_t* dst = obase + (int64_t)r * a.son + cc * 8;
+        if (a.o16) {
+          st16(dst, v);
+        } else {
+          st8(dst, u32x2{v[0], v[1]});
+          st8(dst + 4, u32x2{v[2], v[3]});
+        }
+      }
     }
   }
-  if (a.lse != nullptr && g == 0) {
+  if (row_ok && a.lse != nullptr && g == 0) {
     // natural-log LSE (triton_fwd.py:169-172)
     a.lse[(int64_t)b * a.slb + (int64_t)hq * a.slh + (qtok0 + qi)] = (m_run + __log2f(l_safe)) * kLn2;
   }
@@ -458,6 +494,8 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
   a.sob = p.o_stride_b;
   a.soh = p.o_stride_h;
   a.son = p.o_stride_n;
+  a.o16 = (reinterpret_cast<uintptr_t>(p.o) % 16 == 0 && p.o_stride_h % 8 == 0 && p.o_stride_n % 8 == 0 &&
+           (varlen || p.o_stride_b % 8 == 0)) ? 1 : 0;
   a.lse = p.lse;
   a.slb = p.lse_stride_b;
   a.slh = p.lse_stride_h;
