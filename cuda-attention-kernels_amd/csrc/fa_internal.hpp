@@ -46,6 +46,7 @@ struct TileArgs {
   // (partition-major: the rows one workgroup writes for one partition are one block)
   int32_t part_major;
   int32_t o16;  // prefill: O base and strides allow 16-byte stores
+  int32_t u_heads, u_items;  // dense prefill schedule: q-heads per scheduling unit, and times n_rowblk
 };
 
 struct QuantArgs {

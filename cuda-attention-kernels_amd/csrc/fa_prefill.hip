@@ -29,6 +29,8 @@
 // block apart from that and the rare online-softmax rescale.
 #include <float.h>
 
+#include <algorithm>
+
 #include <type_traits>
 
 #include "fa_device.hpp"
@@ -79,6 +81,17 @@ attn_fwd_kernel(const TileArgs a) {
   __shared__ __align__(16) uint16_t v_buf1[VTILE];
 
   // ---- work item: (batch, q-head, NW*32-query block) ----------------------------------
+  // One scalar load per 64-byte line of the argument block, all issued at entry: left to the
+  // compiler, the fields are loaded where they are first used, in four dependent round trips
+  // before the first DMA can go out.
+  {
+    const uint32_t* ap = reinterpret_cast<const uint32_t*>(&a);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(TileArgs) / 4); i += 16) {
+      const uint32_t x = ap[i];
+      __asm__ volatile("" ::"s"(x));
+    }
+  }
   PrefillItem it;
   if (!prefill_item<D>(a, it)) return;  // grid padding (uniform over the workgroup)
   const int b = it.b, hq = it.hq, kvh = it.kvh, rb = it.rb;
@@ -135,15 +148,15 @@ attn_fwd_kernel(const TileArgs a) {
   const float c = fmaxf(fabsf(a.qk_scale), kMinScale);
 
   // ---- Q fragments (B operand of S^T), resident for the whole kernel ----------------
-  // (rows past the end read row 0, which exists, and are zeroed).  They are loaded in the
-  // prologue after the first K/V tiles' DMA is issued, so that both latencies overlap.
+  // (rows past the end read row 0, which exists, and are zeroed).  They are loaded right
+  // after the first K/V tiles' DMA is issued, so that both latencies overlap, and fixed up
+  // (sign, rows past the end) only once the rest of the set-up is done.
   u32x4 qf[KS];
   auto load_q = [&]() __attribute__((always_inline)) {
     const int64_t qrow = qtok0 + (row_ok ? qi : 0);
     const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.sqb + (int64_t)hq * a.sqh + qrow * a.sqn + 8 * g;
-    const uint32_t keep = row_ok ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = (ld16(qp + 16 * s) ^ qsign) & keep;
+    for (int s = 0; s < KS; ++s) qf[s] = ld16(qp + 16 * s);
   };
 
   // ---- K/V tiles: global -> LDS --------------------------------------------------------
@@ -183,6 +196,16 @@ attn_fwd_kernel(const TileArgs a) {
 #pragma unroll
     for (int i = 0; i < VQPW; ++i) dma_v(rv, dst, i);
   };
+
+  // ---- prologue, first half: K_0, V_0, K_1 and then Q go out before the rest of the set-up
+  if (n_tiles > 0) {
+    load_k(0, k_buf0);
+    load_v(0, v_buf0);
+    if (n_tiles > 1) load_k(BN, k_buf1);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  load_q();
+  __builtin_amdgcn_sched_barrier(0);
 
   // Per-lane LDS element offsets of the MFMA operand reads.
   // K: S^T A-operand, row kb*32 + j, logical chunk 2s + g.
@@ -374,14 +397,12 @@ attn_fwd_kernel(const TileArgs a) {
   };
 
   // ---- prologue: K_0, V_0, K_1 in flight; S_0 and its max ------------------------------
+  {
+    const uint32_t keep = row_ok ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = (qf[s] ^ qsign) & keep;
+  }
   if (n_tiles > 0) {
-    load_k(0, k_buf0);
-    load_v(0, v_buf0);
-    if (n_tiles > 1) load_k(BN, k_buf1);
-    // the Q loads go out behind the DMA (the sign/row fix-up waits for them, and would
-    // otherwise hold the DMA back by a memory round trip)
-    __builtin_amdgcn_sched_barrier(0);
-    load_q();
     lds_dma_wait();
     __syncthreads();
 #pragma unroll
@@ -528,6 +549,9 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
   }
   a.total = (int32_t)total;
   a.kv_groups = (int32_t)kv_groups;
+  // a unit never holds more than the (batch, q-head) pairs there are, which keeps u_items <= total
+  a.u_heads = (int32_t)std::min<int64_t>(prefill_unit_heads(a.nk, p.head_dim, a.group), kv_groups * a.group);
+  a.u_items = a.u_heads * a.n_rowblk;
   a.n_split = 1;
   a.split_len = 0;
   hipError_t e = hipErrorInvalidValue;

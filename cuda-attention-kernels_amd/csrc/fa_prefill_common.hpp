@@ -31,36 +31,50 @@ struct PrefillItem {
 // together and read its K/V through one L2 (measured: +8-10% over rank-major across all
 // XCDs, which fetched each K/V tile into up to four L2s).  The host pads the grid to a
 // multiple of 8 groups; padding returns false.
+// K/V bytes of the q-heads one dense scheduling unit holds (one XCD's L2).
+constexpr int64_t kL2UnitBytes = int64_t{4} << 20;
+
+// q-heads per dense scheduling unit: the q-heads of as many whole kv-heads as fit kL2UnitBytes.
+// The host computes it once per launch (TileArgs::u_heads).
+inline int prefill_unit_heads(int nk, int head_dim, int group) {
+  const int64_t kv_head_bytes = (int64_t)(nk > 1 ? nk : 1) * head_dim * 2 * 2;
+  const int64_t kv_heads = kL2UnitBytes / kv_head_bytes;
+  return (int)(kv_heads > 1 ? kv_heads : 1) * group;
+}
+
 template <int D>
 __device__ __forceinline__ bool prefill_item(const TileArgs& a, PrefillItem& it) {
-  constexpr int64_t kL2UnitBytes = int64_t{4} << 20;
-  constexpr int kXcds = 8;
-  int mrev, item;
+  // Every quantity here is non-negative: unsigned division needs no sign fix-ups, and all
+  // waves of the workgroup run this scalar code before their first DMA.
+  constexpr uint32_t kXcds = 8;
+  const uint32_t group = (uint32_t)a.group, bid = blockIdx.x;
+  uint32_t mrev, item;
   if (a.varlen) {
-    const int xcd = (int)blockIdx.x % kXcds, local = (int)blockIdx.x / kXcds;
-    const int per_rank = a.total / (a.n_rowblk * kXcds);  // this XCD's (group, q-head) items per rank
+    const uint32_t xcd = bid % kXcds, local = bid / kXcds;
+    const uint32_t per_rank = (uint32_t)a.total / ((uint32_t)a.n_rowblk * kXcds);  // this XCD's items per rank
     mrev = local / per_rank;
-    const int j = local % per_rank;
-    const int kvg = (j / a.group) * kXcds + xcd;
-    if (kvg >= a.kv_groups) return false;
-    item = kvg * a.group + j % a.group;
+    const uint32_t j = local - mrev * per_rank;
+    const uint32_t jg = j / group;
+    const uint32_t kvg = jg * kXcds + xcd;
+    if (kvg >= (uint32_t)a.kv_groups) return false;
+    item = kvg * group + (j - jg * group);
   } else {
-    const int nbh = a.total / a.n_rowblk;  // (batch, q-head) pairs
-    const int logical = xcd_remap((int)blockIdx.x, a.total);
-    const int64_t kv_head_bytes = (int64_t)max(a.nk, 1) * D * 2 * 2;
-    const int unit_heads = max(1, (int)(kL2UnitBytes / kv_head_bytes)) * a.group;
-    const int unit = logical / (unit_heads * a.n_rowblk);
-    const int within = logical % (unit_heads * a.n_rowblk);
-    const int unit_size = min(unit_heads, nbh - unit * unit_heads);
+    const uint32_t nbh = (uint32_t)a.kv_groups * group;  // (batch, q-head) pairs
+    const uint32_t logical = (uint32_t)xcd_remap((int)bid, a.total);
+    const uint32_t unit_heads = (uint32_t)a.u_heads;  // prefill_unit_heads(nk, D, group)
+    const uint32_t unit = logical / (uint32_t)a.u_items;
+    const uint32_t within = logical - unit * (uint32_t)a.u_items;
+    const uint32_t unit_size = min(unit_heads, nbh - unit * unit_heads);
     mrev = within / unit_size;
-    item = unit * unit_heads + within % unit_size;
+    item = unit * unit_heads + (within - mrev * unit_size);
   }
-  const int gi = item % a.group;
-  item /= a.group;
-  it.kvh = item % a.hkv;
-  it.b = item / a.hkv;
-  it.hq = it.kvh * a.group + gi;
-  it.rb = a.causal ? (a.n_rowblk - 1 - mrev) : mrev;  // heaviest causal blocks first
+  const uint32_t kvi = item / group;
+  const uint32_t gi = item - kvi * group;
+  const uint32_t bb = kvi / (uint32_t)a.hkv;
+  it.kvh = (int)(kvi - bb * (uint32_t)a.hkv);
+  it.b = (int)bb;
+  it.hq = it.kvh * a.group + (int)gi;
+  it.rb = a.causal ? (a.n_rowblk - 1 - (int)mrev) : (int)mrev;  // heaviest causal blocks first
   return true;
 }
 
