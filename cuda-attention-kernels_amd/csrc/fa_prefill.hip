@@ -529,15 +529,17 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
     a.sqb = a.skb = a.svb = a.sob = a.slb = 0;  // rows are addressed by packed token index
   }
   if (a.nq <= 0 || p.batch <= 0) return FA_OK;
-  // Dense D=128 with at least 4096 queries runs 8 waves (256 queries) per workgroup: each K/V
-  // tile feeds twice the rows, halving the DMA per MFMA (measured over 4 waves, Hq=32 Hkv=8:
-  // +1% causal at N=4096, +2% at 8192 and 16384).  Shorter sequences keep 4 (more, shorter
-  // workgroups: 8 waves lose 8% causal at N=1024, 2% at 2048).  D=64 keeps 4 (-3% with 8) and
-  // D=256 runs one wave per SIMD.  Varlen follows the longest sequence (max_seqlen_q): the
-  // 16-sequence batch with lengths up to 4096 gains 1.3% with 8 waves, although its short
-  // sequences leave part of a 256-query block empty.  A wave computes the same tiles in the same
-  // order with 4 or 8 waves per workgroup, so the result does not depend on the choice.
-  const int nw = (p.head_dim == 128 && a.nq >= 4096) ? 8 : 4;
+  // Dense D=128 with at least 4096 queries (2048 without the causal mask) runs 8 waves (256
+  // queries) per workgroup: each K/V tile feeds twice the rows, halving the DMA per MFMA
+  // (measured over 4 waves, Hq=32 Hkv=8: +1% causal at N=4096, +2% at 8192 and 16384, +1.7%
+  // non-causal at 2048).  Shorter sequences keep 4 (more, shorter workgroups whose start
+  // overlaps the other workgroup on the CU: 8 waves lose 5% causal at N=1024, 2.5% at 2048,
+  // 0.7% non-causal at 1024).  D=64 keeps 4 (-3% with 8) and D=256 runs one wave per SIMD.
+  // Varlen follows the longest sequence (max_seqlen_q): the 16-sequence batch with lengths up
+  // to 4096 gains 1.3% with 8 waves, although its short sequences leave part of a 256-query
+  // block empty.  A wave computes the same tiles in the same order with 4 or 8 waves per
+  // workgroup, so the result does not depend on the choice.
+  const int nw = (p.head_dim == 128 && a.nq >= (p.causal ? 4096 : 2048)) ? 8 : 4;
   a.n_rowblk = (a.nq + nw * 32 - 1) / (nw * 32);
   const int64_t kv_groups = (int64_t)p.batch * p.heads_kv;
   // varlen: the (sequence, kv-head) groups are padded to a multiple of the 8 XCDs

@@ -226,10 +226,12 @@ def test_long_context_prefill(causal):
 
 
 @pytest.mark.parametrize("n_q,n_k,causal", [(4200, 5000, True), (4096, 3000, True), (4100, 4100, False),
-                                            (5000, 4200, True)])
+                                            (5000, 4200, True), (2048, 3000, False), (2500, 777, False),
+                                            (4095, 4095, True)])
 def test_eight_wave_blocks_ragged_and_offset(n_q, n_k, causal):
-    """Dense D=128 with >= 4096 queries runs 256-query workgroups: a partial last block, bottom-right
-    causal offsets both ways (rows that see no key when n_k < n_q) and the per-wave causal skip."""
+    """Dense D=128 with >= 4096 queries (>= 2048 without the causal mask) runs 256-query workgroups: a
+    partial last block, bottom-right causal offsets both ways (rows that see no key when n_k < n_q) and
+    the per-wave causal skip.  4095 causal queries stay on the 4-wave kernel, next to its limit."""
     announce(f"8-wave prefill nq={n_q} nk={n_k} causal={causal}")
     gen = torch.Generator(device="cuda").manual_seed(n_q + n_k)
     q = randn(1, 8, n_q, 128, dtype=torch.bfloat16, gen=gen)
