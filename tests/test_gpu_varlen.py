@@ -66,6 +66,27 @@ def test_varlen_writes_only_sequence_rows():
     assert max_err(out[:total], ref[:total]) <= TOL[torch.bfloat16]
 
 
+@pytest.mark.parametrize("lens", [[3, 0, 130, 1, 64], [4096, 17, 300]])
+def test_varlen_output_with_8_byte_alignment_only(lens):
+    """An output view whose base and head stride are 8-byte but not 16-byte aligned takes the kernel's
+    8-byte store path: same bits as a fresh output, and the columns around the view keep their sentinel."""
+    announce(f"varlen 8-byte aligned output lens={lens}")
+    torch.manual_seed(1)
+    total = sum(lens)
+    q = randn(total, 8, 128, dtype=torch.bfloat16)
+    k = randn(total, 2, 128, dtype=torch.bfloat16)
+    v = randn(total, 2, 128, dtype=torch.bfloat16)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+    ref = _hip.varlen_fwd(q, k, v, cu, cu, max(lens), max(lens), causal=True)
+    buf = torch.full((total, 8, 132), float("nan"), dtype=torch.bfloat16, device="cuda")
+    out = buf[:, :, 4:132]
+    assert out.data_ptr() % 16 == 8 and (out.stride(1) * 2) % 16 == 8
+    _hip.varlen_fwd(q, k, v, cu, cu, max(lens), max(lens), causal=True, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert torch.isnan(buf[:, :, :4]).all()
+
+
 def test_benchmark_varlen_workload():
     """16 sequences, lengths ~U[0, 4096] by seed with one 0 and one 1; Hq=32, Hkv=8, D=128, bf16, causal."""
     announce("benchmark varlen")
