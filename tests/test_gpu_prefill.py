@@ -241,3 +241,29 @@ def test_eight_wave_blocks_ragged_and_offset(n_q, n_k, causal):
     ref = orc.attention_chunked(q, k, v, causal=causal, heads_per_chunk=2, rows_per_chunk=1024)
     assert not torch.isnan(out).any()
     assert max_err(out, ref) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("n_q,n_k,causal", [(4200, 5000, True), (2500, 777, False)])
+def test_eight_wave_blocks_fp16_with_lse(n_q, n_k, causal):
+    """The 8-wave workgroups in fp16, with the LSE output: rows of a partial last block and rows that
+    see no key (n_k < n_q) included."""
+    announce(f"8-wave prefill fp16 + LSE nq={n_q} nk={n_k} causal={causal}")
+    gen = torch.Generator(device="cuda").manual_seed(7 * n_q + n_k)
+    q = randn(1, 8, n_q, 128, dtype=torch.float16, gen=gen)
+    k = randn(1, 2, n_k, 128, dtype=torch.float16, gen=gen)
+    v = randn(1, 2, n_k, 128, dtype=torch.float16, gen=gen)
+    out, lse = _hip.fwd(q, k, v, causal=causal, return_lse=True)
+    ref = orc.attention_chunked(q, k, v, causal=causal, heads_per_chunk=2, rows_per_chunk=1024)
+    assert not torch.isnan(out).any()
+    assert max_err(out, ref) <= TOL[torch.float16]
+    # LSE against a float64 log-sum-exp of the same scores (rows with no key: -inf)
+    qd, kd = q.double().cpu(), orc.expand_kv(k.double().cpu(), 4)
+    s = torch.matmul(qd, kd.transpose(-1, -2)) / math.sqrt(128)
+    if causal:
+        s = s.masked_fill(~orc.causal_mask(n_q, n_k), float("-inf"))
+    ref_lse = torch.logsumexp(s, dim=-1).float()
+    got = lse.cpu()
+    finite = torch.isfinite(ref_lse)
+    assert torch.equal(finite, torch.isfinite(got))
+    # l sums the fp16-rounded P (resolution 2^-11); bound the LSE error by 2^-9
+    assert (got[finite] - ref_lse[finite]).abs().max().item() < 2.0 ** -9
