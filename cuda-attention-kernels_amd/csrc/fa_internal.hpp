@@ -42,6 +42,11 @@ struct TileArgs {
   int64_t sbt;       // block_table row stride
   int64_t spk, spv;  // page strides of the K and V pools
   int32_t page_size, num_pages;
+  // key n -> page slot n / page_size as ((uint64_t)n * page_magic) >> page_magic_shift (exact for
+  // n < 2^31: page_magic = ceil(2^page_magic_shift / page_size), page_magic_shift = 31 +
+  // ceil(log2(page_size)))
+  uint32_t page_magic;
+  int32_t page_magic_shift;
   // split-K partial layout: 0 = [B, Hq, Nq, S, D] (row-major), 1 = [B, Hkv, S, G*Nq, D]
   // (partition-major: the rows one workgroup writes for one partition are one block)
   int32_t part_major;

@@ -279,9 +279,13 @@ attn_splitk_kernel(const TileArgs a) {
   // keep the Q loads ahead of the first K/V tiles' DMA: waiting for Q then leaves the tiles in flight
   __builtin_amdgcn_sched_barrier(0);
 
+  // page slot of key n >= 0: a multiply-high in place of a division by the page size
+  auto slot_of = [&](int n) __attribute__((always_inline)) {
+    return (int)(((uint64_t)(uint32_t)n * a.page_magic) >> a.page_magic_shift);
+  };
   // page of key n (paged; n in [klo, khi), so its slot is among the loaded entries)
   auto page_of = [&](int n) __attribute__((always_inline)) {
-    const int rel = __builtin_amdgcn_readfirstlane(n / a.page_size - first_slot);
+    const int rel = __builtin_amdgcn_readfirstlane(slot_of(n) - first_slot);
     const int ln = rel & 63;
     int v = __builtin_amdgcn_readlane(pg[0], ln);
     if (rel >= 64) v = __builtin_amdgcn_readlane(pg[1], ln);
@@ -298,7 +302,7 @@ attn_splitk_kernel(const TileArgs a) {
       const int valid = min(khi - nh, PGS);
       const int page = valid <= 0 ? -1 : (n0 == klo ? first_pages[h] : page_of(nh));
       const bool ok = valid > 0 && (uint32_t)page < (uint32_t)a.num_pages;
-      const int64_t off = ok ? (int64_t)(nh % a.page_size) : 0;
+      const int64_t off = ok ? (int64_t)(nh - slot_of(nh) * a.page_size) : 0;
       const int64_t pgk = ok ? (int64_t)page * a.spk : 0, pgv = ok ? (int64_t)page * a.spv : 0;
       const uint32_t klim = __builtin_amdgcn_readfirstlane(
           ok ? (uint32_t)(valid - 1) * (uint32_t)krow_bytes + (uint32_t)(D * KV::bytes) : 0u);
@@ -511,7 +515,7 @@ attn_splitk_kernel(const TileArgs a) {
           const int nk = n0 + kb * 32;
           const int page = nk < khi ? page_of(nk) : -1;
           const bool ok = (uint32_t)page < (uint32_t)a.num_pages;
-          const int64_t at = ok ? (int64_t)page * a.ssb + (nk % a.page_size) / 64 : 0;
+          const int64_t at = ok ? (int64_t)page * a.ssb + (nk - slot_of(nk) * a.page_size) / 64 : 0;
           ks = ok ? ksc[at] : 0.f;
           vsv = ok ? vsc[at] : 0.f;
         } else {
@@ -972,6 +976,10 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
     a.spv = kv->v_page_stride;
     a.page_size = kv->page_size;
     a.num_pages = kv->num_pages;
+    int lg = 0;
+    while ((1 << lg) < kv->page_size) ++lg;
+    a.page_magic_shift = 31 + lg;
+    a.page_magic = (uint32_t)(((uint64_t{1} << a.page_magic_shift) + (uint64_t)kv->page_size - 1) / (uint64_t)kv->page_size);
   }
   if (p.batch <= 0 || p.seqlen_q <= 0) return FA_OK;
   const int S = p.seqlen_k > 0 ? (p.seqlen_k + split_len - 1) / split_len : 1;
