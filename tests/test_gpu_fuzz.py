@@ -60,6 +60,31 @@ def test_fuzz_dense(seed):
     check_bars(out, ref, _tol(dtype))
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_fuzz_dense_long(seed):
+    """D=128 with 2048-5000 queries: the 256-query (8-wave) workgroups, with ragged last row
+    blocks and key tiles, both layouts, custom and negative scales."""
+    rng = random.Random(7000 + seed)
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    hkv = rng.choice([1, 2])
+    hq = hkv * rng.choice([1, 2])
+    causal = rng.random() < 0.5
+    n_q = rng.randint(4096 if causal else 2048, 5000)
+    n_k = rng.choice([rng.randint(1, 700), rng.randint(2000, 5000)])
+    bnhd = rng.random() < 0.4
+    scale = rng.choice([None, None, 0.05, -0.1])
+    announce(f"fuzz dense long seed={seed} {dtype} hq={hq} hkv={hkv} nq={n_q} nk={n_k} causal={causal} "
+             f"bnhd={bnhd} scale={scale}")
+    torch.manual_seed(7000 + seed)
+    q = _tensor((1, hq, n_q, 128), dtype, bnhd)
+    k = _tensor((1, hkv, n_k, 128), dtype, bnhd)
+    v = _tensor((1, hkv, n_k, 128), dtype, bnhd)
+    out = fused_attn.attention(q, k, v, causal=causal, scale=scale)
+    ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=causal, scale=scale)
+    assert out.shape == q.shape and out.dtype == dtype
+    check_bars(out, ref, _tol(dtype))
+
+
 @pytest.mark.parametrize("seed", range(32))
 def test_fuzz_splitk(seed):
     rng = random.Random(1000 + seed)
