@@ -60,7 +60,7 @@ def test_fuzz_dense(seed):
     check_bars(out, ref, _tol(dtype))
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(24))
 def test_fuzz_dense_long(seed):
     """D=128 with 2048-5000 queries: the 256-query (8-wave) workgroups, with ragged last row
     blocks and key tiles, both layouts, custom and negative scales."""
@@ -145,6 +145,35 @@ def test_fuzz_varlen(seed):
     qs = [randn(n, hq, d, dtype=dtype) for n in lens_q]
     ks = [randn(n, hkv, d, dtype=dtype) for n in lens_k]
     vs = [randn(n, hkv, d, dtype=dtype) for n in lens_k]
+    q, cu_q, max_q = fused_attn.pack_varlen(qs)
+    k, cu_k, max_k = fused_attn.pack_varlen(ks)
+    v, _, _ = fused_attn.pack_varlen(vs)
+    out = fused_attn.attention_varlen(q, k, v, cu_q, cu_k, max_q, max_k, causal=causal)
+    ref = orc.attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=causal)
+    assert out.shape == q.shape
+    check_bars(out, ref, _tol(dtype))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_fuzz_varlen_long(seed):
+    """Varlen D=128 batches whose longest sequence reaches the 256-query (8-wave) workgroups,
+    beside empty, one-token and short sequences."""
+    rng = random.Random(8000 + seed)
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    hkv = rng.choice([1, 2])
+    hq = hkv * rng.choice([1, 2])
+    causal = rng.random() < 0.5
+    nseq = rng.randint(2, 5)
+    lens_q = [rng.choice([0, 1, rng.randint(2, 700), rng.randint(700, 4600)]) for _ in range(nseq)]
+    lens_q[rng.randrange(nseq)] = rng.randint(4096 if causal else 2048, 4600)
+    same = rng.random() < 0.5
+    lens_k = list(lens_q) if same else [rng.randint(0, 4600) for _ in range(nseq)]
+    announce(f"fuzz varlen long seed={seed} {dtype} hq={hq} hkv={hkv} lens_q={lens_q} lens_k={lens_k} "
+             f"causal={causal}")
+    torch.manual_seed(8000 + seed)
+    qs = [randn(n, hq, 128, dtype=dtype) for n in lens_q]
+    ks = [randn(n, hkv, 128, dtype=dtype) for n in lens_k]
+    vs = [randn(n, hkv, 128, dtype=dtype) for n in lens_k]
     q, cu_q, max_q = fused_attn.pack_varlen(qs)
     k, cu_k, max_k = fused_attn.pack_varlen(ks)
     v, _, _ = fused_attn.pack_varlen(vs)
