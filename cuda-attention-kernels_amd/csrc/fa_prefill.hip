@@ -539,10 +539,11 @@ fa_status run_fwd(const fa_fwd_params& p, bool varlen, hipStream_t stream, const
   // non-causal at 2048).  Shorter sequences keep 4 (more, shorter workgroups whose start
   // overlaps the other workgroup on the CU: 8 waves lose 5% causal at N=1024, 2.5% at 2048,
   // 0.7% non-causal at 1024).  D=64 keeps 4 (-3% with 8) and D=256 runs one wave per SIMD.
-  // Varlen follows the longest sequence (max_seqlen_q): the 16-sequence batch with lengths up
-  // to 4096 gains 1.3% with 8 waves, although its short sequences leave part of a 256-query
-  // block empty.  A wave computes the same tiles in the same order with 4 or 8 waves per
-  // workgroup, so the result does not depend on the choice.
+  // Varlen applies the same rule to its longest sequence (max_seqlen_q): a causal batch of 16
+  // sequences of 0-4073 tokens keeps 4 waves, and 8 from 2048 measured 2-5% slower on it (its
+  // short sequences leave more of a 256-query block empty).  A wave computes the same tiles
+  // in the same order with 4 or 8 waves per workgroup, so the result does not depend on the
+  // choice.
   const int nw = (p.head_dim == 128 && a.nq >= (p.causal ? 4096 : 2048)) ? 8 : 4;
   a.n_rowblk = (a.nq + nw * 32 - 1) / (nw * 32);
   const int64_t kv_groups = (int64_t)p.batch * p.heads_kv;
