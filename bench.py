@@ -283,7 +283,8 @@ def bench_decode(steps, warmup, only_128=False):
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
+            "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_events": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
     if only_128:
         return res
@@ -299,7 +300,8 @@ def bench_decode(steps, warmup, only_128=False):
                     f"n_k={c['nk']} D={c['d']} bf16 (context: no key split)",
         "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
         "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
+        "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_events": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
     }
     res.update(bench_paged(k, v, steps, warmup, g))
     res.update(bench_paged(k, v, steps, warmup, g, page_size=16, splits=(128,), suffix="_16key_pages"))
@@ -325,7 +327,8 @@ def bench_decode(steps, warmup, only_128=False):
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
+            "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_events": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
     # the same FP8 cache scattered into a shuffled pool of 64-key pages with per-page block scales
     kc, vc, ksp, vsp, bt, sl = fused_attn.paged_from_dense_fp8(k8, ks, v8, vs, 64,
@@ -343,12 +346,95 @@ def bench_decode(steps, warmup, only_128=False):
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
+            "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_events": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
     del q, k8, ks, v8, vs, kd0, vd0, kc, vc, ksp, vsp
     torch.cuda.empty_cache()
     res.update(bench_decode_d256(steps, warmup, g))
     return res
+
+
+DECODE_SWEEP = dict(b=1, hq=32, hkv=8, d=128, ctx=(4096, 16384, 65536))
+PREFILL_SWEEP = dict(b=2, hq=32, hkv=8, d=128, n=(2048, 8192, 16384))
+
+
+def bench_decode_sweep(steps, warmup):
+    """Single-sequence decode across context lengths (the reference's decode benchmark,
+    benchmarks/bench_decode.py:30-65: batch 1, Hq=32, Hkv=8, D=128, one fp16 query, causal, contexts
+    4096/16384/65536): the single-pass prefill kernel, split-K with the reference's split heuristic
+    (choose_num_splits over the GPU's 256 CUs), split-K with the op's default partitions, and the FP8
+    KV cache at its default partitions.  GB/s counts each variant's own K/V (+ scale) bytes."""
+    import torch
+
+    import fused_attn
+    from fused_attn.fp8 import dequantize_kv_fp8
+    from fused_attn.triton_fwd import attention_triton
+
+    c = DECODE_SWEEP
+    g = torch.Generator(device="cuda").manual_seed(0)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    res = {}
+    for n in c["ctx"]:
+        q = torch.randn(c["b"], c["hq"], 1, c["d"], device="cuda", generator=g).half()
+        k = torch.randn(c["b"], c["hkv"], n, c["d"], device="cuda", generator=g).half()
+        v = torch.randn(c["b"], c["hkv"], n, c["d"], device="cuda", generator=g).half()
+        k8, ks = fused_attn.quantize_kv_fp8(k)
+        v8, vs = fused_attn.quantize_kv_fp8(v)
+        kd, vd = dequantize_kv_fp8(k8, ks), dequantize_kv_fp8(v8, vs)
+        kv16 = 2 * k.numel() * 2
+        kv8 = 2 * k8.numel() + 2 * ks.numel() * 4
+        splits = fused_attn.choose_num_splits(c["b"], c["hq"], n, 1, cus)
+        default = fused_attn.ops.default_split_len(1, n, c["b"], c["hkv"], c["hq"] // c["hkv"])
+        variants = (
+            ("single_pass", "single-pass prefill kernel (no key split)",
+             lambda: attention_triton(q, k, v, causal=True), kv16, (k, v)),
+            ("splitk_ref_heuristic", f"split-K, {splits} splits (the reference's choose_num_splits over {cus} CUs)",
+             lambda: fused_attn.attention_splitk(q, k, v, causal=True, num_splits=splits), kv16, (k, v)),
+            ("splitk_default", f"split-K, {default}-key partitions (the op's default policy)",
+             lambda: fused_attn.attention(q, k, v, causal=True), kv16, (k, v)),
+            ("fp8_kv", "FP8-KV split-K (e4m3fn + fp32 per-64-key scales), default partitions",
+             lambda: fused_attn.attention_fp8(q, k8, ks, v8, vs, causal=True), kv8, (kd, vd)),
+        )
+        row = {}
+        for name, what, fn, nbytes, (kr, vr) in variants:
+            err = _ref_err(fn(), q, kr, vr, True)
+            wall, ev = _time_calls(fn, steps, warmup)
+            row[name] = {"workload": what, "ms": round(wall * 1e3, 4), "ms_events": round(ev * 1e3, 4),
+                         "GB_s": round(nbytes / wall / 1e9, 1), "bytes": nbytes,
+                         "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err}
+        res[f"ctx{n}"] = row
+        del q, k, v, k8, ks, v8, vs, kd, vd
+        torch.cuda.empty_cache()
+    return {"workload": f"decode B={c['b']} Hq={c['hq']} Hkv={c['hkv']} n_q=1 D={c['d']} fp16 causal, contexts "
+                        f"{'/'.join(map(str, c['ctx']))}", **res}
+
+
+def bench_prefill_sweep(steps, warmup):
+    """The reference README's prefill table shape (README.md:167-175, filled by benchmarks/bench.py:64-127):
+    causal bf16 B=2 Hq=32 Hkv=8 D=128 at N = 2048, 8192, 16384."""
+    import torch
+
+    import fused_attn
+
+    c = PREFILL_SWEEP
+    g = torch.Generator(device="cuda").manual_seed(0)
+    res = {}
+    for n in c["n"]:
+        q = torch.randn(c["b"], c["hq"], n, c["d"], device="cuda", generator=g).bfloat16()
+        k = torch.randn(c["b"], c["hkv"], n, c["d"], device="cuda", generator=g).bfloat16()
+        v = torch.randn(c["b"], c["hkv"], n, c["d"], device="cuda", generator=g).bfloat16()
+        fn = lambda: fused_attn.attention(q, k, v, causal=True)  # noqa: E731
+        err = _slice_err(fn(), q, k, v, True)
+        wall, ev = _time_calls(fn, steps, warmup)
+        flops = attn_flops(c["b"], c["hq"], n, c["d"], True)
+        res[f"N{n}"] = {"ms": round(wall * 1e3, 4), "ms_events": round(ev * 1e3, 4),
+                        "TFLOP_s": round(flops / wall / 1e12, 1), "TFLOP_s_events": round(flops / ev / 1e12, 1),
+                        "mfma_frac": round(flops / wall / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4), "max_abs_err": err}
+        del q, k, v
+        torch.cuda.empty_cache()
+    return {"workload": f"causal prefill B={c['b']} Hq={c['hq']} Hkv={c['hkv']} D={c['d']} bf16, "
+                        f"N={'/'.join(map(str, c['n']))}", **res}
 
 
 def bench_decode_d256(steps, warmup, g):
@@ -369,7 +455,8 @@ def bench_decode_d256(steps, warmup, g):
         "workload": f"split-K B={b} Hq={hq} Hkv={hkv} n_q=1 n_k={nk} D={d} bf16, 128-key partitions + LSE combine",
         "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
         "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_events": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
     }}
     del q, k, v
     torch.cuda.empty_cache()
@@ -399,7 +486,8 @@ def bench_paged(k, v, steps, warmup, g, page_size=64, splits=(128, None), suffix
                         f"{'' if split else ' (default partition policy)'}",
             "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
             "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-            "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
+            "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_events": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4), "max_abs_err": err,
         }
     return res
 
@@ -430,7 +518,8 @@ def bench_quantize(steps, warmup):
         "kernel": "quantize_kv_fp8_kernel<bf16,128>",
         "ms": round(wall * 1e3, 4), "GB_s": round(nbytes / wall / 1e9, 1),
         "GB_s_events": round(nbytes / ev / 1e9, 1), "bytes": nbytes,
-        "hbm_frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_events": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
         "mismatches_vs_torch_chain": mismatches,
     }
 
@@ -508,6 +597,10 @@ def run_only(which, steps, warmup):
         print(f"prefill: {flops / ev / 1e12:.1f} TFLOP/s kernel, {ev * 1e3:.4f} ms", flush=True)
     elif which == "prefill_other":
         print(json.dumps(bench_prefill_extras(steps, warmup)), flush=True)
+    elif which == "prefill_sweep":
+        print(json.dumps(bench_prefill_sweep(steps, warmup)), flush=True)
+    elif which == "decode_sweep":
+        print(json.dumps(bench_decode_sweep(steps, warmup)), flush=True)
     elif which == "quantize":
         print(json.dumps(bench_quantize(steps, warmup)), flush=True)
     elif which in ("decode", "decode128"):
@@ -524,7 +617,8 @@ def main():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
-    p.add_argument("--only", choices=["prefill", "prefill_other", "decode", "decode128", "quantize", "copy"],
+    p.add_argument("--only", choices=["prefill", "prefill_other", "prefill_sweep", "decode", "decode128",
+                                      "decode_sweep", "quantize", "copy"],
                    default=None,
                    help="run one workload without the JSON line (for profiler runs)")
     a = p.parse_args()
@@ -569,8 +663,10 @@ def main():
     }
     line["context"] = {"sdpa": sdpa}
     line["prefill_other"] = bench_prefill_extras(max(5, a.steps // 2), max(2, a.warmup))
+    line["prefill_sweep"] = bench_prefill_sweep(max(5, a.steps // 2), max(2, a.warmup))
     if not a.no_decode:
         line["decode"] = bench_decode(max(5, a.steps), max(2, a.warmup))
+        line["decode_sweep"] = bench_decode_sweep(max(5, a.steps), max(2, a.warmup))
         line["quantize"] = bench_quantize(max(5, a.steps), max(2, a.warmup))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

@@ -205,6 +205,8 @@ fa_status fa_attention_paged_decode(const fa_fwd_params* p, const fa_paged_kv* k
     return fail(FA_ERR_INVALID_ARGUMENT, "split_len must be a positive multiple of 64");
   if (kv->page_size <= 0 || kv->page_size % 16 != 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "page_size must be a positive multiple of 16");
+  if (kv->page_size > FA_MAX_PAGE_SIZE)
+    return fail(FA_ERR_INVALID_ARGUMENT, "page_size must be at most 2^24 keys");
   const bool fp8 = q.kv_dtype == FA_DTYPE_FP8_E4M3;
   if (fp8 && kv->page_size % 64 != 0)
     return fail(FA_ERR_INVALID_ARGUMENT, "FP8 pools need page_size a multiple of 64 (64-key scale blocks)");

@@ -191,27 +191,21 @@ attn_splitk_kernel(const TileArgs a) {
   const int64_t krow_bytes = a.skn * KV::bytes, vrow_bytes = a.svn * KV::bytes;
   const float* ksc = nullptr;
   const float* vsc = nullptr;
-  // FP8: P is multiplied by v_scale / v_ref before its 16-bit rounding, with v_ref the largest
-  // V block scale of this workgroup's keys, and v_ref goes back in, in fp32, when a partial is
-  // emitted.  The reference applies v_scale after the product, in fp32 (fp8.py:104,116);
-  // folding v_scale itself into P would push P * v_scale (v_scale = amax / 448) below fp16's
-  // normal range for V of small magnitude.  The ratio is at most 1, and only blocks whose
-  // weight is negligible beside the largest lose bits.
-  float v_ref = 1.f;
+  // FP8: the accumulator holds O / v_cur, v_cur being the V block scale of a recent tile, and
+  // v_cur goes back in, in fp32, when a partial is emitted.  A tile whose V block scale vb lies
+  // within a factor 2 of v_cur folds vb / v_cur (in [1/2, 2]) into P before P's 16-bit rounding;
+  // any other tile first re-expresses the accumulator in its own scale (O *= v_cur / vb, fp32),
+  // so P is never scaled by more than 2 either way.  The reference multiplies each block's
+  // P*V by v_scale after the product, in fp32 (fp8.py:116); folding v_scale itself into P would
+  // push P * v_scale (v_scale = amax / 448) into fp16's subnormal range for V of small
+  // magnitude, and folding a ratio to a workgroup-wide maximum scale would do the same for
+  // small-V blocks that sit beside a large-V block.
+  float v_cur = IS_FP8 ? 0.f : 1.f;
   if (KV::bytes == 1) {
     // (paged: the scale pools' base for this kv-head; a block's scale is at page * ssb + its
     // 64-key block inside the page)
     ksc = a.k_scale + (PAGED ? 0 : (int64_t)b * a.ssb) + (int64_t)kvh * a.ssh;
     vsc = a.v_scale + (PAGED ? 0 : (int64_t)b * a.ssb) + (int64_t)kvh * a.ssh;
-    if constexpr (!PAGED) {
-      const int blo = klo / 64, bhi = khi > klo ? (khi + 63) / 64 : blo;
-      float vm = 0.f;
-      for (int bk = blo + (int)(threadIdx.x & 63); bk < bhi; bk += 64) vm = fmaxf(vm, vsc[bk]);
-      vm = max_xor32(vm);
-#pragma unroll
-      for (int sh = 16; sh >= 1; sh >>= 1) vm = fmaxf(vm, __shfl_xor(vm, sh, 64));
-      v_ref = fmaxf(vm, FLT_MIN);
-    }
   }
 
   // A negative softmax scale is applied by negating Q (exact for 16-bit floats),
@@ -243,27 +237,6 @@ attn_splitk_kernel(const TileArgs a) {
     for (int r = 0; r < PG_REGS; ++r) {
       const int sl = first_slot + 64 * r + (tid & 63);
       pg[r] = sl < slot_end ? bt[sl] : -1;
-    }
-    if constexpr (IS_FP8) {
-      // v_ref over the V block scales of keys [klo, khi): lane i looks at the pages its
-      // entries hold (slots first_slot + i + 64 r), page_size / 64 blocks each
-      const int bpp = a.page_size / 64;
-      float vm = 0.f;
-#pragma unroll
-      for (int r = 0; r < PG_REGS; ++r) {
-        const int sl = first_slot + 64 * r + (tid & 63);
-        const int page = pg[r];
-        if ((uint32_t)page < (uint32_t)a.num_pages) {
-          for (int wb = 0; wb < bpp; ++wb) {
-            const int key = (sl * bpp + wb) * 64;
-            if (key >= klo && key < khi) vm = fmaxf(vm, vsc[(int64_t)page * a.ssb + wb]);
-          }
-        }
-      }
-      vm = max_xor32(vm);
-#pragma unroll
-      for (int sh = 16; sh >= 1; sh >>= 1) vm = fmaxf(vm, __shfl_xor(vm, sh, 64));
-      v_ref = fmaxf(vm, FLT_MIN);
     }
   }
   // ---- Q fragments (B operand of S^T), resident for the whole kernel -------------
@@ -415,7 +388,7 @@ attn_splitk_kernel(const TileArgs a) {
   // A partition with no visible key (l = 0) stores zeros.
   auto emit_partial = [&](int part, uint8_t* stage = nullptr) __attribute__((always_inline)) {
     const float l_tot = sum_xor32(l_run);  // each lane summed its 16 of the row's keys per tile
-    const float inv = l_tot > 0.f ? v_ref / l_tot : 0.f;
+    const float inv = l_tot > 0.f ? v_cur / l_tot : 0.f;
     const int vr = min(32, R - wr0);  // rows of this wave
     // partition-major: this wave's rows of the partition are vr consecutive rows
     const int64_t prow0 = ((int64_t)(b * a.hkv + kvh) * a.n_split + part) * R + wr0;
@@ -524,11 +497,27 @@ attn_splitk_kernel(const TileArgs a) {
           vsv = vsc[blk];
         }
         sc[kb] = fmaxf(c_abs * ks, kMinScale);
-        vs[kb] = vsv / v_ref;
+        vs[kb] = vsv;
       } else {
         sc[kb] = c_abs;
         vs[kb] = 1.f;
       }
+    }
+    // FP8: the factor folded into P.  Tiles start at multiples of 64 keys and hold at most 64,
+    // so vs[0] is the tile's one V block scale (0 for keys outside the pool, which are zero
+    // keys: then nothing is folded in and nothing rescaled).
+    float vfold = 1.f;
+    if constexpr (IS_FP8) {
+      static_assert(BN <= 64, "one FP8 scale block per tile");
+      const float vb = vs[0];
+      if (vb > 0.f && !(vb <= 2.f * v_cur && v_cur <= 2.f * vb)) {
+        // re-express O in this block's scale (O is 0 while v_cur is still 0)
+        const float ratio = v_cur / vb;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) oacc[d] *= ratio;
+        v_cur = vb;
+      }
+      vfold = v_cur > 0.f ? vb / v_cur : 0.f;
     }
 
     // Masked tiles (the causal diagonal, the key tail) set excluded scores to -inf
@@ -582,8 +571,9 @@ attn_splitk_kernel(const TileArgs a) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         if constexpr (KV::bytes == 1) {
-          // v_scale / v_ref folded into P (v_ref is restored when the partial is emitted)
-          const float v = vs[kb];
+          // v_scale / v_cur folded into P (v_cur is restored when the partial is emitted); the
+          // row sum takes the unscaled fp32 P, as the reference's tl.sum(p, 1) (fp8.py:113)
+          const float v = vfold;
 #pragma unroll
           for (int e = 0; e < 8; ++e) rs += p[8 * h + e];
           pf[kb][h] = u32x4{pack2<E>(p[8 * h + 0] * v, p[8 * h + 1] * v), pack2<E>(p[8 * h + 2] * v, p[8 * h + 3] * v),
@@ -976,8 +966,8 @@ fa_status run_splitk(const fa_fwd_params& p, int32_t split_len, void* workspace,
     a.spv = kv->v_page_stride;
     a.page_size = kv->page_size;
     a.num_pages = kv->num_pages;
-    int lg = 0;
-    while ((1 << lg) < kv->page_size) ++lg;
+    int lg = 0;  // ceil(log2(page_size)); page_size <= 2^24 (C ABI)
+    while ((int64_t{1} << lg) < (int64_t)kv->page_size) ++lg;
     a.page_magic_shift = 31 + lg;
     a.page_magic = (uint32_t)(((uint64_t{1} << a.page_magic_shift) + (uint64_t)kv->page_size - 1) / (uint64_t)kv->page_size);
   }

@@ -289,12 +289,43 @@ def _prep_qkv(q, k, v, kv_fp8: bool = False):
 
 
 def _new_output(q: torch.Tensor) -> torch.Tensor:
-    # empty_like keeps q's strides when q is dense (e.g. a [B,N,H,D] transpose view), as
-    # torch::empty_like does in the reference (csrc/bindings.cpp:56).
-    o = torch.empty_like(q)
-    if o.stride(-1) != 1 or any(o.size(i) > 1 and o.stride(i) % 4 for i in range(o.dim() - 1)):
-        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    return o
+    """A contiguous output of q's shape and dtype, whatever q's strides.
+
+    The custom ops' fake kernels return ``q.new_empty(q.shape)`` (fused_attn/ops.py:102-104), which
+    is contiguous, and Inductor checks a custom op's real output against the fake's strides.  The
+    reference's ``torch::empty_like`` (csrc/bindings.cpp:56) keeps a ``[B,N,H,D]`` view's strides
+    instead, so a compiled graph fed such a view would fail that check; a contiguous output keeps
+    eager and compiled calls alike.  The kernels write through the output's strides either way."""
+    return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+
+
+def _check_out(out: torch.Tensor, q: torch.Tensor) -> None:
+    """A caller-provided output must be what the kernels write: q's shape, dtype and device, unit
+    D stride, 8-byte aligned with 8-byte strides (the C ABI's rule for o).  Checked before anything
+    is launched, since a smaller buffer would be written past its end."""
+    if tuple(out.shape) != tuple(q.shape):
+        raise RuntimeError(f"out must have q's shape {tuple(q.shape)}, got {tuple(out.shape)}")
+    if out.dtype != q.dtype:
+        raise RuntimeError(f"out must have q's dtype {q.dtype}, got {out.dtype}")
+    if out.device != q.device:
+        raise RuntimeError(f"out must be on {q.device}, got {out.device}")
+    vec = 8 // out.element_size()
+    if out.numel() and (out.stride(-1) != 1 or out.data_ptr() % 8
+                        or any(out.size(i) > 1 and out.stride(i) % vec for i in range(out.dim() - 1))):
+        raise RuntimeError("out needs a unit D stride, an 8-byte aligned start and strides of whole 8-byte words")
+
+
+def _check_lse_out(lse: torch.Tensor, shape: tuple, device: torch.device) -> None:
+    """A caller-provided LSE: fp32 of the given shape on the device, unit stride along the last dim
+    (the kernels write it through its first two strides)."""
+    if tuple(lse.shape) != tuple(shape):
+        raise RuntimeError(f"lse must have shape {tuple(shape)}, got {tuple(lse.shape)}")
+    if lse.dtype != torch.float32:
+        raise RuntimeError(f"lse must be float32, got {lse.dtype}")
+    if lse.device != device:
+        raise RuntimeError(f"lse must be on {device}, got {lse.device}")
+    if lse.numel() and (lse.size(-1) > 1 and lse.stride(-1) != 1 or lse.stride(0) < 0 or lse.stride(1) < 0):
+        raise RuntimeError("lse needs a unit stride along its last dim")
 
 
 def _stride(t: torch.Tensor, i: int) -> int:
@@ -366,6 +397,8 @@ def fwd(q, k, v, causal: bool = False, scale: Optional[float] = None, return_lse
         out: Optional[torch.Tensor] = None):
     """Dense FA2 forward.  q [B,Hq,Nq,D]; k, v [B,Hkv,Nk,D]; returns o (and natural-log LSE [B,Hq,Nq])."""
     _check_qkv(q, k, v, "dense")
+    if out is not None:
+        _check_out(out, q)
     _require_gpu(q, k, v)
     lib = load_library()
     scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
@@ -385,6 +418,8 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqle
     With ``return_lse`` also returns the natural-log LSE as fp32 [Hq, Tq]; rows of tokens outside every
     sequence are left unwritten (like the output rows)."""
     _check_qkv(q, k, v, "varlen")
+    if out is not None:
+        _check_out(out, q)
     _require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k)
     if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
         raise RuntimeError("cu_seqlens must be int32")
@@ -478,12 +513,22 @@ SPLITK_NOALLOC_MAX_BYTES = 64 << 20  # FA_SPLITK_NOALLOC_MAX_BYTES
 
 def splitk_noalloc(q, k, v, causal: bool = False, scale: Optional[float] = None, split_len: int = 128,
                    k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None,
-                   out: Optional[torch.Tensor] = None, return_lse: bool = False):
+                   out: Optional[torch.Tensor] = None, return_lse: bool = False,
+                   lse: Optional[torch.Tensor] = None):
     """``splitk`` through fa_attention_splitk_noalloc: the library uses its own static per-GPU workspace
-    (at most SPLITK_NOALLOC_MAX_BYTES) and allocates nothing; calls overlapping on one GPU race.  ``out``
-    (and the LSE) are the caller's to provide for a call that must allocate nothing either."""
+    (at most SPLITK_NOALLOC_MAX_BYTES) and allocates nothing; calls overlapping on one GPU race.
+
+    A call that must allocate nothing passes ``out`` ([B,Hq,Nq,D] in q's dtype) and, for the LSE,
+    ``lse`` (fp32 [B,Hq,Nq], implies ``return_lse``), with q/k/v (and FP8 scales) already in the
+    kernels' layout (unit D stride, 16-byte aligned rows), so that nothing is copied either.  Both are
+    checked against q before anything is launched.  Without them they are allocated here."""
     fp8 = _FP8 is not None and k.dtype == _FP8
     _check_qkv(q, k, v, "dense", kv_fp8=fp8)
+    if out is not None:
+        _check_out(out, q)
+    if lse is not None:
+        _check_lse_out(lse, q.shape[:3], q.device)
+        return_lse = True
     if fp8:
         _check_fp8_scales(k, k_scale, v_scale)
     _require_gpu(q, k, v)
@@ -493,7 +538,8 @@ def splitk_noalloc(q, k, v, causal: bool = False, scale: Optional[float] = None,
     if fp8:
         k_scale, v_scale = _prep_fp8_scales(k, k_scale, v_scale)
     o = _new_output(q) if out is None else out
-    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if return_lse else None
+    if return_lse and lse is None:
+        lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
     p = make_params(q, k, v, o, causal, scale, k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None,
                     lse=lse)
     with torch.cuda.device(q.device):

@@ -12,9 +12,14 @@ On the GPU the quantiser is one fused HIP kernel (one workgroup per 64-key
 block) whose bytes and scales are bit-identical to the reference's torch chain on
 the GPU; CPU tensors, or ``FUSED_ATTN_BACKEND=reference``, run that torch chain.
 The dequantiser is the reference's torch chain.  ``attention_fp8`` runs the
-HIP split-K kernel, which converts each E4M3 element exactly to q's 16-bit type
-as it stages K/V through LDS, multiplies the score block by
-``scale * k_scale`` and folds ``v_scale`` into P before the PV product.  Any
+HIP split-K kernel, which keeps K/V 8-bit in LDS and widens each E4M3 element
+exactly to q's 16-bit type as it reads an MFMA operand, and multiplies the score
+block by ``scale * k_scale``.  For V it keeps the fp32 accumulator in units of a
+recent block's ``v_scale`` (v_cur): a block whose scale is within a factor 2 of
+v_cur folds ``v_scale / v_cur`` into P before P's 16-bit rounding, any other
+block first rescales the accumulator to its own scale, and v_cur multiplies the
+result in fp32.  This is the reference's ``P.V * v_scale`` per block
+(fp8.py:116) up to fp32 rounding, with P never scaled by more than 2.  Any
 number of queries is accepted (prefill-shaped calls too).
 """
 from __future__ import annotations

@@ -3,11 +3,13 @@
 Decode contributes one or a few query rows per request, so a one-pass kernel
 has too few workgroups to stream a long K/V cache at full HBM bandwidth.  The
 keys are cut into partitions of ``split_len`` keys (a multiple of 64); each
-partition runs the online-softmax loop and writes an un-normalised fp32 partial
-output plus its log2-domain (max, sum); a combine kernel merges them exactly:
+partition runs the online-softmax loop and writes an fp32 partial output
+normalised by its own row sum (Ô_s = O_s / l_s, a convex combination of V rows)
+plus its log2-domain (max, sum); a combine kernel merges them exactly:
 
-    m = max_s m_s,   l = sum_s 2^(m_s - m) l_s,   O = sum_s 2^(m_s - m) O_s / l
+    m = max_s m_s,   l = sum_s 2^(m_s - m) l_s,   O = sum_s 2^(m_s - m) l_s Ô_s / l
 
+which is the reference's merge of un-normalised partials O_s = l_s Ô_s
 (reference: fused_attn/triton_splitk.py:1-16,90-127).  On MI355X one workgroup
 covers a (batch, kv-head, partition): all Hq/Hkv query heads that share the
 kv-head are rows of the same tile, so the K/V cache is read once from HBM.

@@ -135,6 +135,8 @@ fa_status fa_attention_splitk(const fa_fwd_params* p, int32_t split_len, void* w
 #define FA_SPLITK_NOALLOC_MAX_BYTES ((size_t)64 << 20)
 fa_status fa_attention_splitk_noalloc(const fa_fwd_params* p, int32_t split_len, void* stream);
 
+#define FA_MAX_PAGE_SIZE (1 << 24) /* largest page_size fa_attention_paged_decode accepts */
+
 /* Paged (block-table) K/V for fa_attention_paged_decode.  The K and V pools hold
    num_pages pages of page_size keys; p->k / p->v point at the pools and
    p->k_stride_h / k_stride_n (v likewise) are the head and key strides inside a
@@ -144,7 +146,8 @@ typedef struct fa_paged_kv {
   const int32_t* block_table;  /* [batch, block_table_cols] page indices, on the device */
   int64_t block_table_stride;  /* elements between rows of block_table */
   int32_t block_table_cols;    /* pages per sequence in the table; cols * page_size >= p->seqlen_k */
-  int32_t page_size;           /* keys per page: a positive multiple of 16 (64 for FP8 pools) */
+  int32_t page_size;           /* keys per page: a positive multiple of 16 (64 for FP8 pools), at most
+                                  FA_MAX_PAGE_SIZE */
   const int32_t* seqlens_k;    /* [batch] keys per sequence, on the device; values above p->seqlen_k
                                   are read as p->seqlen_k, negative values as 0 */
   int32_t num_pages;           /* pages per pool; a table entry outside [0, num_pages) reads as zero keys */

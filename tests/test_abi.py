@@ -297,6 +297,9 @@ def test_paged_struct_layout(lib):
 @pytest.mark.parametrize("kv_over,p_over,split,code,msg", [
     (dict(page_size=40), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "multiple of 16"),
     (dict(page_size=0), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "multiple of 16"),
+    # beyond FA_MAX_PAGE_SIZE (2^24 keys): rejected before the page-slot magic number is derived
+    (dict(page_size=(1 << 24) + 16), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "at most 2^24"),
+    (dict(page_size=(1 << 31) - 16), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "at most 2^24"),
     (dict(num_pages=-1), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "negative"),
     (dict(block_table_cols=3), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "fewer pages"),
     (dict(block_table=0), {}, 128, _hip.FA_ERR_INVALID_ARGUMENT, "non-NULL"),

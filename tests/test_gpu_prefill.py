@@ -66,8 +66,8 @@ def test_noncontiguous_bnhd_layout(dtype):
     assert not q.is_contiguous()
     out = fused_attn.attention(q, k, v, causal=True)
     ref = orc.attention(q.cpu(), k.cpu(), v.cpu(), causal=True)
-    # empty_like: a dense output in q's dim order ([B,N,H,D] storage), as torch::empty_like gives
-    assert out.shape == q.shape and out.stride() == (64 * 4 * 64, 64, 4 * 64, 1)
+    # a contiguous [B,H,N,D] output, the strides of the op's fake (q.new_empty(q.shape))
+    assert out.shape == q.shape and out.is_contiguous()
     assert max_err(out, ref) <= TOL[dtype]
 
 

@@ -130,3 +130,36 @@ def test_valid_cpu_inputs_reach_the_gpu_requirement():
         _hip.fwd(t(2, 8, 16, 64), t(2, 2, 32, 64), t(2, 2, 32, 64))
     with pytest.raises(RuntimeError, match="needs GPU tensors"):
         _hip.splitk(t(2, 8, 1, 64), t(1, 2, 4096, 64), t(1, 2, 4096, 64))
+
+
+OUT_BAD = [
+    # (out, message fragment) for q = [2, 8, 1, 64] bf16
+    (t(2, 8, 1, 32), "shape"),
+    (t(2, 8, 2, 64), "shape"),
+    (t(2, 8, 1, 64, dtype=torch.float16), "dtype"),
+    (t(2, 8, 1, 128)[..., ::2], "unit D stride"),
+    (t(2 * 8 * 64 + 1)[1:].view(2, 8, 1, 64), "8-byte"),
+]
+
+
+@pytest.mark.parametrize("out,msg", OUT_BAD)
+def test_caller_outputs_are_checked_before_launch(out, msg):
+    """A caller's ``out`` smaller than q, or of another dtype or layout, would be written past its end:
+    the no-allocation path and the prefill entry points reject it before the C ABI."""
+    q, k = t(2, 8, 1, 64), t(2, 2, 4096, 64)
+    with pytest.raises(RuntimeError, match=msg):
+        _hip.splitk_noalloc(q, k, k, out=out)
+    with pytest.raises(RuntimeError, match=msg):
+        _hip.fwd(q, k, k, out=out)
+
+
+def test_caller_lse_is_checked_before_launch():
+    q, k = t(2, 8, 1, 64), t(2, 2, 4096, 64)
+    for lse, msg in [(torch.zeros(2, 8), "shape"), (torch.zeros(2, 8, 1, dtype=torch.float16), "float32"),
+                     (torch.zeros(2, 8, 2)[..., :1].transpose(0, 1).contiguous().transpose(0, 1), None)]:
+        if msg is None:  # a permuted but unit-stride LSE is accepted; the call then needs the GPU
+            with pytest.raises(RuntimeError, match="GPU"):
+                _hip.splitk_noalloc(q, k, k, lse=lse)
+            continue
+        with pytest.raises(RuntimeError, match=msg):
+            _hip.splitk_noalloc(q, k, k, lse=lse)

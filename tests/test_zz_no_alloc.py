@@ -65,3 +65,30 @@ def test_noalloc_rejects_requests_beyond_its_array():
     out = _hip.splitk_noalloc(q, k, k, split_len=4096)
     torch.cuda.synchronize()
     assert torch.equal(out, _hip.splitk(q, k, k, split_len=4096))
+
+
+def test_noalloc_with_caller_out_and_lse_allocates_nothing():
+    """With the output and the LSE passed in, the call allocates no device memory: neither torch's
+    allocator nor the device's free bytes change across it (after one warm-up call, whose first
+    launch may load the kernels' code objects).  The results still equal the workspace entry point's."""
+    announce("noalloc: caller out and lse, no allocation")
+    gen = torch.Generator(device="cuda").manual_seed(23)
+    q = randn(2, 8, 1, 128, dtype=torch.bfloat16, gen=gen)
+    k = randn(2, 2, 3000, 128, dtype=torch.bfloat16, gen=gen)
+    v = randn(2, 2, 3000, 128, dtype=torch.bfloat16, gen=gen)
+    want, want_lse = _hip.splitk(q, k, v, split_len=256, return_lse=True)
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    _hip.splitk_noalloc(q, k, v, split_len=256, out=out, lse=lse)
+    out.zero_()
+    lse.zero_()
+    torch.cuda.synchronize()
+    alloc0 = torch.cuda.memory_allocated()
+    free0, _ = torch.cuda.mem_get_info()
+    got, got_lse = _hip.splitk_noalloc(q, k, v, split_len=256, out=out, lse=lse)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert torch.cuda.memory_allocated() == alloc0
+    assert free1 == free0
+    assert got is out and got_lse is lse
+    assert torch.equal(out, want) and torch.equal(lse, want_lse)
