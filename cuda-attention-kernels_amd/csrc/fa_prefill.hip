@@ -44,6 +44,15 @@
 
 namespace fa {
 
+// Compile-time loop: f(integral_constant<int, I>) for I in [I0, N), always fully unrolled.
+template <int I0, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I0 < N) {
+    f(std::integral_constant<int, I0>{});
+    static_for<I0 + 1, N>(f);
+  }
+}
+
 template <int D, class E, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 attn_fwd_kernel(const TileArgs a) {
@@ -211,22 +220,24 @@ attn_fwd_kernel(const TileArgs a) {
   load_q();
   __builtin_amdgcn_sched_barrier(0);
 
-  // Per-lane LDS element offsets of the MFMA operand reads.
+  // Per-lane LDS byte offsets of the MFMA operand reads.  Unsigned, so that the compiler may
+  // fold the buffer bases and the per-slot constants into the ds_read offset field instead of
+  // holding one address register per (buffer, slot) pair (16 VGPRs at D=128).
   // K: S^T A-operand, row kb*32 + j, logical chunk 2s + g.
-  int koffs[KS];
+  uint32_t koffs[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) koffs[s] = j * D + (((2 * s + g) ^ Shape::swz_k(j)) * 8);
+  for (int s = 0; s < KS; ++s) koffs[s] = (uint32_t)(j * D + (((2 * s + g) ^ Shape::swz_k(j)) * 8)) * 2u;
   // V: ds_read_b64_tr_b16 sources, rows 8g + 4*hi + (i >> 2) of each 16-key step,
   // columns 32d + 16dh + 4(i & 3); the row term kb*32 + 16h is a constant offset.
   const int tr_i = lane & 15, tr_dh = (lane >> 4) & 1;
-  int voffs[DB][2];
+  uint32_t voffs[DB][2];
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
     for (int hi = 0; hi < 2; ++hi) {
       const int vr_row = 8 * g + 4 * hi + (tr_i >> 2);
       const int col = 32 * d + 16 * tr_dh + 4 * (tr_i & 3);
-      voffs[d][hi] = vr_row * DV + (((col >> 3) ^ VShape::swz_v(vr_row)) * 8) + (col & 7);
+      voffs[d][hi] = (uint32_t)(vr_row * DV + (((col >> 3) ^ VShape::swz_v(vr_row)) * 8) + (col & 7)) * 2u;
     }
   }
 
@@ -243,7 +254,8 @@ attn_fwd_kernel(const TileArgs a) {
   // ---- building blocks ---------------------------------------------------------------
   auto qk = [&](const uint16_t* Ks, f32x16(&acc)[KB], int s) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma32<E>(ld16(Ks + kb * 32 * D + koffs[s]), qf[s], acc[kb]);
+    for (int kb = 0; kb < KB; ++kb)
+      acc[kb] = mfma32<E>(ld16((const uint8_t*)Ks + (kb * 32 * D * 2 + koffs[s])), qf[s], acc[kb]);
   };
   // excluded scores of tile t (keys n0..n0+BN) -> -inf
   auto mask = [&](f32x16(&sc)[KB], int n0) __attribute__((always_inline)) {
@@ -319,12 +331,12 @@ attn_fwd_kernel(const TileArgs a) {
     auto read = [&](int m) __attribute__((always_inline)) {
       if (m < NQK) {
         const int s = m / KB, kb = m % KB;
-        opnd[m % (PD + 1)] = ld16(Kn + kb * 32 * D + koffs[s]);
+        opnd[m % (PD + 1)] = ld16((const uint8_t*)Kn + (kb * 32 * D * 2 + koffs[s]));
       } else {
         const int i = m - NQK, kb = i / (2 * DB), h = (i / DB) % 2, d = i % DB;
-        const uint16_t* vp = Vc + (kb * 32 + 16 * h) * DV;
-        const u32x2 lo = lds_read_tr16(vp + voffs[d][0]);
-        const u32x2 hi = lds_read_tr16(vp + voffs[d][1]);
+        const uint8_t* vp = (const uint8_t*)Vc + (kb * 32 + 16 * h) * DV * 2;
+        const u32x2 lo = lds_read_tr16((const uint16_t*)(vp + voffs[d][0]));
+        const u32x2 hi = lds_read_tr16((const uint16_t*)(vp + voffs[d][1]));
         opnd[m % (PD + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
     };
@@ -344,42 +356,41 @@ attn_fwd_kernel(const TileArgs a) {
       mx = vmax(vmax(mx, nxt[kb][r]), nxt[kb][r + 1]);  // one v_maximum3 per two scores
     };
 
-#pragma unroll
-    for (int m = 0; m < PD; ++m) read(m);
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      if (m + PD < NM) read(m + PD);
-      if (m < NDMA) {
-        const int i = m;
-        if (i < QPW) {
-          dma_k(rk, kd, i);
+    // (static_for: every slot index is a compile-time constant, so the operand ring, the
+    // accumulator indices and the LDS offsets resolve without relying on loop unrolling)
+    static_for<0, PD>([&](auto mc) __attribute__((always_inline)) { read(decltype(mc)::value); });
+    static_for<0, NM>([&](auto mc) __attribute__((always_inline)) {
+      constexpr int m = decltype(mc)::value;
+      if constexpr (m + PD < NM) read(m + PD);
+      if constexpr (m < NDMA) {
+        if constexpr (m < QPW) {
+          dma_k(rk, kd, m);
         } else {
-          dma_v(rv, vd, i - QPW);
+          dma_v(rv, vd, m - QPW);
         }
       }
       const u32x4 op = opnd[m % (PD + 1)];
-      if (m < NQK) {
-        const int s = m / KB, kb = m % KB;
+      if constexpr (m < NQK) {
+        constexpr int s = m / KB, kb = m % KB;
         nxt[kb] = mfma32<E>(op, qf[s], nxt[kb]);
-#pragma unroll
-        for (int u = 0; u < NEXP; ++u) {
-          if (u * NQK / NEXP == m) exp_step(u);
-        }
+        static_for<0, NEXP>([&](auto uc) __attribute__((always_inline)) {
+          constexpr int u = decltype(uc)::value;
+          if constexpr (u * NQK / NEXP == m) exp_step(u);
+        });
       } else {
-        const int i = m - NQK, kb = i / (2 * DB), h = (i / DB) % 2, d = i % DB;
+        constexpr int i = m - NQK, kb = i / (2 * DB), h = (i / DB) % 2, d = i % DB;
         oacc[d] = mfma32<E>(op, pf[kb][h], oacc[d]);
         if constexpr (MFMA_ROWSUM) {
-          if (d == 0) l_acc = mfma16<E>(ones, pf[kb][h], l_acc);  // row sums of 16 keys of P_t
+          if constexpr (d == 0) l_acc = mfma16<E>(ones, pf[kb][h], l_acc);  // row sums of 16 keys of P_t
         }
         // S_{t+1} is complete two slots after its last MFMA was issued
-        const int v0 = (i - 2) * NMAX / (NPV - 2), v1 = (i - 1) * NMAX / (NPV - 2);
-        if (i >= 2) {
-#pragma unroll
-          for (int v = v0; v < v1; ++v) max_step(v);
+        if constexpr (i >= 2) {
+          constexpr int v0 = (i - 2) * NMAX / (NPV - 2), v1 = (i - 1) * NMAX / (NPV - 2);
+          static_for<v0, v1>([&](auto vc) __attribute__((always_inline)) { max_step(decltype(vc)::value); });
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
     l_run += rs;
     float mt = max_xor32(mx * c);
     if (t + 1 >= n_fast) {
