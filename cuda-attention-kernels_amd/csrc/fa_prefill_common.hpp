@@ -16,12 +16,12 @@ struct PrefillItem {
 
 // Workgroup blockIdx.x -> work item; false for grid padding (varlen), uniform over the workgroup.
 //
-// Dense: scheduling units are the q-heads of as many kv-heads as keep about kL2UnitBytes of
-// K/V (one XCD's L2 is 4 MB).  Units follow each other in logical order, and xcd_remap hands
-// each XCD a contiguous range of logical indices, so an XCD works through one or two units at
-// a time and re-reads K/V from its L2.  Inside a unit the query blocks go by rank, heaviest
-// causal blocks first, all heads of the unit at each rank, which keeps the XCD's CUs evenly
-// loaded to the end.
+// Dense: scheduling units are the q-heads of as many kv-heads as keep about unit_bytes of
+// K/V (prefill_unit_bytes; one XCD's L2 is 4 MB).  Units follow each other in logical order, and
+// xcd_remap hands each XCD a contiguous range of logical indices, so an XCD works through one
+// or two units at a time and re-reads K/V from its L2.  Inside a unit the query blocks go by
+// rank, heaviest causal blocks first, all heads of the unit at each rank, which keeps the
+// XCD's CUs evenly loaded to the end.
 //
 // Varlen: sequences differ in length, and ranges of whole sequences per XCD load the XCDs
 // unevenly (measured: a 16-sequence batch ran at 0.18 of peak).  There the order is
@@ -31,14 +31,20 @@ struct PrefillItem {
 // together and read its K/V through one L2 (measured: +8-10% over rank-major across all
 // XCDs, which fetched each K/V tile into up to four L2s).  The host pads the grid to a
 // multiple of 8 groups; padding returns false.
-// K/V bytes of the q-heads one dense scheduling unit holds (one XCD's L2).
-constexpr int64_t kL2UnitBytes = int64_t{4} << 20;
 
-// q-heads per dense scheduling unit: the q-heads of as many whole kv-heads as fit kL2UnitBytes.
-// The host computes it once per launch (TileArgs::u_heads).
+// K/V bytes of the q-heads one dense scheduling unit holds.  At D=128 half an XCD's L2: the
+// Q and O streams (64 KiB each per 256-row workgroup) pass through the same L2, and a unit
+// whose K/V filled all 4 MB had them evicted and re-fetched (causal GQA B=4 Hq=32 Hkv=8 N=4096:
+// 296 MB read for 201 MB of Q, K and V with 4 MB units, 216 MB with 2 MB units, at the same
+// speed).  At D <= 64 a workgroup's Q and O are half as large or less, and halving the unit
+// cost 2-8% (MHA D=64 N=4096: fewer heads to spread over the XCD's CUs), so those keep 4 MB.
+inline int64_t prefill_unit_bytes(int head_dim) { return int64_t{head_dim == 128 ? 2 : 4} << 20; }
+
+// q-heads per dense scheduling unit: the q-heads of as many whole kv-heads as fit
+// prefill_unit_bytes.  The host computes it once per launch (TileArgs::u_heads).
 inline int prefill_unit_heads(int nk, int head_dim, int group) {
   const int64_t kv_head_bytes = (int64_t)(nk > 1 ? nk : 1) * head_dim * 2 * 2;
-  const int64_t kv_heads = kL2UnitBytes / kv_head_bytes;
+  const int64_t kv_heads = prefill_unit_bytes(head_dim) / kv_head_bytes;
   return (int)(kv_heads > 1 ? kv_heads : 1) * group;
 }
 
