@@ -13,6 +13,7 @@ gfx950 GPU, every entry point raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 import os
@@ -196,6 +197,10 @@ _device_ok: dict[int, bool] = {}
 
 def device_supported(device: torch.device | int | None = None) -> bool:
     """True when the library loads and ``device`` is a gfx950 GPU (has_tensor_core_kernel analogue)."""
+    if isinstance(device, torch.device) and device.index is not None:
+        ok = _device_ok.get(device.index)  # per-call fast path: the answer is fixed per device
+        if ok is not None:
+            return ok
     if not torch.cuda.is_available():
         return False
     if device is None:
@@ -234,6 +239,10 @@ TOKEN_STRIDE_LIMIT_BYTES = 1 << 24  # the C ABI's bound on K/V token strides
 def _aligned_view(t: torch.Tensor, vec_elems: int, base_align: int) -> torch.Tensor:
     """``t`` itself when its D stride is 1 and its pointer/other strides allow the kernels'
     vector accesses, else a contiguous copy (the kernels never see an unaligned view)."""
+    # (fast path: a contiguous tensor's strides are multiples of its last size)
+    if (t.is_contiguous() and t.dim() >= 3 and t.size(-1) % vec_elems == 0 and t.data_ptr() % base_align == 0
+            and t.stride(2 if t.dim() == 4 else 0) * t.element_size() < TOKEN_STRIDE_LIMIT_BYTES):
+        return t
     ok = t.stride(-1) == 1 and t.data_ptr() % base_align == 0
     if ok:
         for i in range(t.dim() - 1):
@@ -337,16 +346,20 @@ def make_params(q, k, v, o, causal: bool, scale: float, *, kv_dtype=None, lse=No
                 cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=0, max_seqlen_k=0) -> FwdParams:
     """Fill ``fa_fwd_params`` from tensors.  Dense: q/o [B,Hq,Nq,D], k/v [B,Hkv,Nk,D].
     Varlen: q/o [Tq,Hq,D], k/v [Tk,Hkv,D] with int32 cu_seqlens of length batch+1."""
-    p = FwdParams()
-    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
     if cu_seqlens_q is None:
-        p.q_stride_b, p.q_stride_h, p.q_stride_n = _stride(q, 0), _stride(q, 1), _stride(q, 2)
-        p.k_stride_b, p.k_stride_h, p.k_stride_n = _stride(k, 0), _stride(k, 1), _stride(k, 2)
-        p.v_stride_b, p.v_stride_h, p.v_stride_n = _stride(v, 0), _stride(v, 1), _stride(v, 2)
-        p.o_stride_b, p.o_stride_h, p.o_stride_n = _stride(o, 0), _stride(o, 1), _stride(o, 2)
-        p.batch, p.heads_q, p.seqlen_q, p.head_dim = q.shape
-        p.heads_kv, p.seqlen_k = k.shape[1], k.shape[2]
+        # one positional constructor call (filled in C) instead of a Python attribute set per field
+        qz, kz, vz, oz = q.shape, k.shape, v.shape, o.shape
+        qs, ks, vs, os_ = q.stride(), k.stride(), v.stride(), o.stride()
+        p = FwdParams(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            qs[0] if qz[0] > 1 else 0, qs[1] if qz[1] > 1 else 0, qs[2] if qz[2] > 1 else 0,
+            ks[0] if kz[0] > 1 else 0, ks[1] if kz[1] > 1 else 0, ks[2] if kz[2] > 1 else 0,
+            vs[0] if vz[0] > 1 else 0, vs[1] if vz[1] > 1 else 0, vs[2] if vz[2] > 1 else 0,
+            os_[0] if oz[0] > 1 else 0, os_[1] if oz[1] > 1 else 0, os_[2] if oz[2] > 1 else 0,
+            qz[0], qz[1], kz[1], qz[2], kz[2], qz[3])
     else:
+        p = FwdParams()
+        p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
         p.q_stride_b = p.k_stride_b = p.v_stride_b = p.o_stride_b = 0
         p.q_stride_h, p.q_stride_n = _stride(q, 1), _stride(q, 0)
         p.k_stride_h, p.k_stride_n = _stride(k, 1), _stride(k, 0)
@@ -371,8 +384,22 @@ def make_params(q, k, v, o, causal: bool, scale: float, *, kv_dtype=None, lse=No
     return p
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """Handle of the current stream of t's device: the stream the op's work goes on."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+_SAME_DEVICE = contextlib.nullcontext()
+
+
+def _on_device(dev: torch.device):
+    """``torch.cuda.device(dev)``, or no device switch at all when ``dev`` is already current."""
+    return _SAME_DEVICE if torch.cuda.current_device() == dev.index else torch.cuda.device(dev)
 
 
 def _require_gpu(*ts: torch.Tensor) -> None:
@@ -406,7 +433,7 @@ def fwd(q, k, v, causal: bool = False, scale: Optional[float] = None, return_lse
     o = _new_output(q) if out is None else out
     lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if return_lse else None
     p = make_params(q, k, v, o, causal, scale, lse=lse)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _check(lib.fa_attention_fwd(ctypes.byref(p), ctypes.c_void_p(_stream(q))), "attention_fwd")
     return (o, lse) if return_lse else o
 
@@ -436,7 +463,7 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqle
     if lse is not None:  # [Hq, Tq]: head stride Tq, unit token stride
         p.lse = lse.data_ptr()
         p.lse_stride_b, p.lse_stride_h = 0, lse.stride(0)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _check(lib.fa_attention_varlen_fwd(ctypes.byref(p), ctypes.c_void_p(_stream(q))), "attention_varlen_fwd")
     return (o, lse) if return_lse else o
 
@@ -501,7 +528,7 @@ def splitk(q, k, v, causal: bool = False, scale: Optional[float] = None, split_l
     lse = torch.empty((b, hq, nq), dtype=torch.float32, device=q.device) if return_lse else None
     p = make_params(q, k, v, o, causal, scale, k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None,
                     lse=lse)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _check(lib.fa_attention_splitk(ctypes.byref(p), int(split_len), ctypes.c_void_p(workspace.data_ptr()),
                                        workspace.numel() * workspace.element_size(),
                                        ctypes.c_void_p(_stream(q))), "attention_splitk")
@@ -542,7 +569,7 @@ def splitk_noalloc(q, k, v, causal: bool = False, scale: Optional[float] = None,
         lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
     p = make_params(q, k, v, o, causal, scale, k_scale=k_scale if fp8 else None, v_scale=v_scale if fp8 else None,
                     lse=lse)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _check(lib.fa_attention_splitk_noalloc(ctypes.byref(p), int(split_len), ctypes.c_void_p(_stream(q))),
                "attention_splitk_noalloc")
     return (o, lse) if return_lse else o
@@ -610,7 +637,7 @@ def paged_decode(q, k_cache, v_cache, block_table, seqlens_k, max_seqlen_k: int,
     kv.page_size, kv.num_pages = k_cache.shape[2], k_cache.shape[0]
     kv.seqlens_k = sl.data_ptr()
     kv.k_page_stride, kv.v_page_stride = _stride(k_cache, 0), _stride(v_cache, 0)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         _check(lib.fa_attention_paged_decode(ctypes.byref(p), ctypes.byref(kv), int(split_len),
                                              ctypes.c_void_p(workspace.data_ptr()),
                                              workspace.numel() * workspace.element_size(),
@@ -649,6 +676,6 @@ def quantize_kv_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     p.x_stride_b, p.x_stride_h, p.x_stride_n = _stride(x, 0), _stride(x, 1), _stride(x, 2)
     p.batch, p.heads, p.seqlen, p.head_dim = b, h, n, d
     p.dtype = _DTYPE_CODE.get(x.dtype, -1) if x.dtype != _FP8 else -1
-    with torch.cuda.device(x.device):
+    with _on_device(x.device):
         _check(lib.fa_quantize_kv_fp8(ctypes.byref(p), ctypes.c_void_p(_stream(x))), "quantize_kv_fp8")
     return x8, scale

@@ -192,6 +192,17 @@ def test_make_params_marshals_strides():
     assert (p.o_stride_b, p.o_stride_h, p.o_stride_n) == q.stride()[:3]
     assert (p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_k, p.head_dim) == (2, 8, 2, 64, 64, 128)
     assert p.causal == 1 and p.dtype == p.kv_dtype == _hip.BF16 and abs(p.scale - 0.5) < 1e-7
+    assert p.lse is None and p.k_scale is None and p.v_scale is None and p.cu_seqlens_q is None
+    # decode shape: size-1 dims are never stepped over and pass stride 0 (q's query dim, a K/V batch
+    # of one broadcast over q's batch)
+    qd = torch.empty(3, 8, 1, 64, dtype=torch.float16)
+    kd = torch.empty(1, 2, 500, 64, dtype=torch.float16)
+    od = torch.empty_like(qd)
+    p = _hip.make_params(qd, kd, kd, od, False, 0.125)
+    assert (p.q_stride_b, p.q_stride_h, p.q_stride_n) == (8 * 64, 64, 0)
+    assert (p.k_stride_b, p.k_stride_h, p.k_stride_n) == (0, 500 * 64, 64)
+    assert (p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_k, p.head_dim) == (3, 8, 2, 1, 500, 64)
+    assert p.causal == 0 and p.dtype == p.kv_dtype == _hip.F16 and p.max_seqlen_q == 0
     # varlen: token stride is dim 0, batch strides unused
     qv = torch.empty(100, 8, 64, dtype=torch.float16)
     kv = torch.empty(90, 2, 64, dtype=torch.float16)
