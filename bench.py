@@ -608,11 +608,52 @@ def run_only(which, steps, warmup):
         print(json.dumps(bench_decode_sweep(steps, warmup)), flush=True)
     elif which == "quantize":
         print(json.dumps(bench_quantize(steps, warmup)), flush=True)
+    elif which == "mfma_ceiling":
+        print(json.dumps(bench_mfma_ceiling(steps, warmup)), flush=True)
     elif which in ("decode", "decode128"):
         print(json.dumps(bench_decode(steps, warmup, only_128=which == "decode128")), flush=True)
     else:
         wall, ev, nbytes = copy_calibration(steps, warmup)
         print(f"copy {nbytes} B: {ev * 1e3:.4f} ms, {2 * nbytes / ev / 1e9:.1f} GB/s read+write", flush=True)
+
+
+CEILING_ITERS = 4000  # rounds of four MFMAs per wave: about 0.6 ms per launch, like the prefill kernel
+
+
+def bench_mfma_ceiling(steps, warmup, prefill_tflops=None):
+    """What the matrix cores sustain on this board: the probe kernel of fa_ceiling.hip (libfa_probe.so)
+    streams independent v_mfma_f32_32x32x16_bf16 on register operands of random bf16 data, eight waves
+    per CU as the 8-wave prefill kernel runs, with no memory, LDS or vector work.  Timed like the other
+    workloads; its rate is the practical ceiling for the prefill loop's matrix work (the board's clock
+    under MFMA load included), beside the spec peak that roofline.frac uses."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "cuda-attention-kernels_amd", "fused_attn", "libfa_probe.so"))
+    lib.fa_probe_mfma_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_void_p]
+    lib.fa_probe_data_elems.restype = ctypes.c_int
+    g = torch.Generator(device="cuda").manual_seed(0)
+    data = torch.randn(lib.fa_probe_data_elems(), device="cuda", generator=g).bfloat16()
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(grid * 512, dtype=torch.float32, device="cuda")
+
+    def launch():
+        rc = lib.fa_probe_mfma_ceiling(ctypes.c_void_p(data.data_ptr()), ctypes.c_void_p(out.data_ptr()), grid,
+                                       CEILING_ITERS, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"mfma ceiling probe launch failed ({rc})")
+
+    wall, ev = _time_calls(launch, steps, warmup)
+    flops = float(grid) * 8 * CEILING_ITERS * 4 * (2 * 32 * 32 * 16)
+    tflops = flops / ev / 1e12
+    res = {"workload": f"v_mfma_f32_32x32x16_bf16 only, register operands of random bf16 data, {grid} workgroups "
+                       f"of 8 waves (one per CU), {CEILING_ITERS} x 4 MFMAs per wave",
+           "TFLOP_s": round(tflops, 1), "ms": round(ev * 1e3, 4), "frac_of_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+    if prefill_tflops is not None:
+        res["prefill_frac_of_ceiling"] = round(prefill_tflops / tflops, 4)
+    return res
 
 
 def main():
@@ -623,7 +664,7 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--only", choices=["prefill", "prefill_other", "prefill_sweep", "decode", "decode128",
-                                      "decode_sweep", "quantize", "copy"],
+                                      "decode_sweep", "quantize", "copy", "mfma_ceiling"],
                    default=None,
                    help="run one workload without the JSON line (for profiler runs)")
     a = p.parse_args()
@@ -668,6 +709,10 @@ def main():
                      "kernel_ms": round(ev * 1e3, 4)},
     }
     line["context"] = {"sdpa": sdpa}
+    try:  # a measurement aid beside the headline: its absence must not cost the bench line
+        line["mfma_ceiling"] = bench_mfma_ceiling(max(5, a.steps // 2), max(2, a.warmup), prefill_tflops=achieved)
+    except (OSError, RuntimeError) as e:
+        line["mfma_ceiling"] = {"error": str(e)}
     line["prefill_other"] = bench_prefill_extras(max(5, a.steps // 2), max(2, a.warmup))
     line["prefill_sweep"] = bench_prefill_sweep(max(5, a.steps // 2), max(2, a.warmup))
     if not a.no_decode:

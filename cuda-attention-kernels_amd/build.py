@@ -1,4 +1,5 @@
-"""Build ``fused_attn/libfused_attn_hip.so`` for gfx950 with hipcc.
+"""Build ``fused_attn/libfused_attn_hip.so`` (and the measurement probe ``fused_attn/libfa_probe.so``)
+for gfx950 with hipcc.
 
     python cuda-attention-kernels_amd/build.py          # or __graft_entry__.build()
 
@@ -19,6 +20,9 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_OUT = os.path.join(HERE, "fused_attn", "libfused_attn_hip.so")
 SOURCES = ["fa_prefill.hip", "fa_prefill_f32.hip", "fa_splitk.hip", "fa_generic.hip", "fa_quant.hip", "fa_abi.cpp"]
+# the matrix-core ceiling probe bench.py times beside the prefill workload: a library of its own
+PROBE_SOURCES = ["fa_ceiling.hip"]
+PROBE_OUT = os.path.join(HERE, "fused_attn", "libfa_probe.so")
 ARCH = os.environ.get("FUSED_ATTN_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -45,20 +49,25 @@ def _run(cmd: list[str]) -> None:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
-    objs = []
     cmds = []
-    for src in SOURCES:
-        obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-        lang = ["-x", "hip"]
-        cmds.append([HIPCC, *COMMON, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+
+    def objects(sources):
+        objs = []
+        for src in sources:
+            obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+            cmds.append([HIPCC, *COMMON, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj])
+            objs.append(obj)
+        return objs
+
+    libs = [(LIB_OUT, objects(SOURCES)), (PROBE_OUT, objects(PROBE_SOURCES))]
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         list(ex.map(_run, cmds))
-    tmp = LIB_OUT + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
-    os.replace(tmp, LIB_OUT)
-    if verbose:
-        print(f"built {LIB_OUT}")
+    for out, objs in libs:
+        tmp = out + ".tmp"
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
+        os.replace(tmp, out)
+        if verbose:
+            print(f"built {out}")
     return LIB_OUT
 
 
